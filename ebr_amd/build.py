@@ -1,0 +1,69 @@
+"""Build recipe of the gfx950 HIP library ``ebr_amd/_lib/libebr_attn.so`` (in-tree, so it travels with the repo).
+
+``python -m ebr_amd.build`` compiles it; ``__graft_entry__.build()`` calls :func:`build`. hipcc cross-compiles for
+gfx950 without a GPU. Packed-fp32 instruction selection is disabled (``-packed-fp32-ops``) for every HIP source.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+OUT_DIR = PKG / "_lib"
+LIB_NAME = "libebr_attn.so"
+ARCH = "gfx950"
+
+SOURCES = [CSRC / "ebr_attn.hip"]
+HEADERS = [CSRC / "attn_tiles.hpp", ROOT / "include" / "ebr_attn.h"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def compile_flags(arch: str = ARCH) -> list:
+    return [
+        f"--offload-arch={arch}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-Wall",
+        "-Wno-unused-function",
+        "-Xclang",
+        "-target-feature",
+        "-Xclang",
+        "-packed-fp32-ops",
+        f"-I{ROOT / 'include'}",
+    ]
+
+
+def build(verbose: bool = False, extra_flags: tuple = ()) -> Path:
+    """Compile every HIP source into the in-tree shared library and return its path."""
+    OUT_DIR.mkdir(parents=True, exist_ok=True)
+    out = OUT_DIR / LIB_NAME
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), *compile_flags(), *extra_flags, *map(str, SOURCES), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+    if verbose and proc.stderr.strip():
+        sys.stderr.write(proc.stderr)
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

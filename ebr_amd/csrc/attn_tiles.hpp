@@ -1,0 +1,308 @@
+// MFMA fragments, LDS chunk staging and lane reductions for the gfx950 attention kernels.
+//
+// Every contraction in the attention path is written as one of two shapes, both on the 16x16 MFMA tile
+// (v_mfma_f32_16x16x32_{bf16,f16} for 16-bit inputs, v_mfma_f32_16x16x4_f32 for fp32):
+//
+//   d-contraction   C[m = x][n = own]  = sum_d X[x][d] * Own[own][d]
+//                   A = rows of the "other side" tensor X from LDS in natural [x][d] layout,
+//                   B = the wave's own 16 rows, kept in registers for the whole pass.
+//   seq-contraction C[m = d][n = own] += sum_x Xt[d][x] * P[x][own]
+//                   A = the other side tensor transposed ([d][x] layout in LDS),
+//                   B = an L x L tile straight out of a d-contraction accumulator.
+//
+// A 16x16 accumulator holds, in lane l, column n = l % 16 and rows m = 4 * (l / 16) + r (r = 0..3). Read as an
+// MFMA B operand, that is "column n = l % 16, k-slots in lane group l / 16" - exactly the B layout - so the L x L
+// tiles never leave registers between the two contractions. For 16-bit inputs a 32-wide k chunk is two such tiles:
+// lane group g holds rows x = 16 h + 4 g + r of tiles h = 0, 1 in k-slots s = 4 h + r. The transposed LDS copy
+// stores column x at position 8 g + 4 h + r so that the matching A operand is one 16-byte LDS read. Which k-slot a
+// value occupies inside the MFMA does not matter for the result: A and B use the same slot for the same x.
+//
+// Chunks of the other side are CH = 32 rows. Rows at or beyond L are zero-filled; the kernels mask what zeros do not
+// neutralise (scores of padded keys).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ebr {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+
+constexpr int CH = 32;                      // other-side rows per LDS chunk
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr int STAT_MAX = 128;               // longest L handled by the one-workgroup-per-(b,h) kernels
+
+template <typename T> struct ET;
+
+template <> struct ET<__bf16> {
+    static constexpr bool F32 = false;
+    static constexpr int VEC = 8;           // elements per 16-byte vector
+    static constexpr int PADN = 8;          // natural layout row padding (elements)
+    static constexpr int PADT = 8;          // transposed layout row padding (elements)
+    using v8 = bf16x8;
+    using v4 = bf16x4;
+    static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0,
+                                                       0);
+    }
+};
+
+template <> struct ET<_Float16> {
+    static constexpr bool F32 = false;
+    static constexpr int VEC = 8;
+    static constexpr int PADN = 8;
+    static constexpr int PADT = 8;
+    using v8 = f16x8;
+    using v4 = f16x4;
+    static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0,
+                                                      0);
+    }
+};
+
+template <> struct ET<float> {
+    static constexpr bool F32 = true;
+    static constexpr int VEC = 4;
+    static constexpr int PADN = 4;
+    static constexpr int PADT = 4;
+};
+
+// Layout constants of one (T, DP) instantiation. DP is the head dimension padded to the d-chunk width.
+template <typename T, int DP> struct Lay {
+    static constexpr int VEC = ET<T>::VEC;
+    static constexpr int CW = 4 * VEC;                   // d covered by one MFMA k step: 32 (16-bit) / 16 (fp32)
+    static constexpr int NC = DP / CW;                   // 16-byte vectors per lane for a full row of D
+    static constexpr int NT = DP / 16;                   // output d tiles of a seq-contraction
+    static constexpr int PN = DP + ET<T>::PADN;          // natural row pitch (elements)
+    static constexpr int PT = CH + ET<T>::PADT;          // transposed row pitch (elements)
+    static constexpr int NATB = CH * PN * (int)sizeof(T);  // bytes of one natural chunk
+    static constexpr int TRB = DP * PT * (int)sizeof(T);   // bytes of one transposed chunk
+    static_assert(DP % CW == 0, "DP must be a multiple of the d-chunk width");
+    static_assert(NATB % 16 == 0 && TRB % 16 == 0, "LDS regions must stay 16-byte aligned");
+};
+
+// Column of chunk-local row x in the transposed LDS layout (see the header comment).
+template <typename T> __device__ __forceinline__ int tr_col(int x) {
+    if constexpr (ET<T>::F32) {
+        return x;
+    } else {
+        return ((x & 15) >> 2) * 8 + (x >> 4) * 4 + (x & 3);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// Lane reductions over the four 16-lane groups (lanes l, l^16, l^32, l^48 hold the same own row).
+// ---------------------------------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ float xsum4(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__device__ __forceinline__ float xmax4(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------------------------------------------------
+// Own-side B fragments: lane (row = own, group g) holds d = c * CW + g * VEC + [0, VEC) for c < NC.
+// ---------------------------------------------------------------------------------------------------------------------
+
+template <typename T, int DP> struct OwnFrag {
+    u32x4 v[Lay<T, DP>::NC];
+};
+
+template <typename T, int DP>
+__device__ __forceinline__ void load_own(OwnFrag<T, DP>& f, const T* base, int64_t srow, int row, int L, int D,
+                                         int g) {
+    using LY = Lay<T, DP>;
+    const T* p = base + (int64_t)row * srow;
+#pragma unroll
+    for (int c = 0; c < LY::NC; ++c) {
+        const int d0 = c * LY::CW + g * LY::VEC;
+        u32x4 z = {0u, 0u, 0u, 0u};
+        f.v[c] = (row < L && d0 < D) ? *reinterpret_cast<const u32x4*>(p + d0) : z;
+    }
+}
+
+// sum_d a[d] * b[d] over this lane's slots, in fp32.
+template <typename T, int DP>
+__device__ __forceinline__ float frag_dot(const OwnFrag<T, DP>& a, const OwnFrag<T, DP>& b) {
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < Lay<T, DP>::NC; ++c) {
+        if constexpr (ET<T>::F32) {
+            const f32x4 x = __builtin_bit_cast(f32x4, a.v[c]);
+            const f32x4 y = __builtin_bit_cast(f32x4, b.v[c]);
+            s += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+        } else {
+            using V8 = typename ET<T>::v8;
+            const V8 x = __builtin_bit_cast(V8, a.v[c]);
+            const V8 y = __builtin_bit_cast(V8, b.v[c]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += (float)x[e] * (float)y[e];
+        }
+    }
+    return s;
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// d-contraction: acc[m = x][n = own] += sum_d Xn[x][d] * Own[own][d] for the 16 rows starting at Xn_tile.
+// ---------------------------------------------------------------------------------------------------------------------
+
+template <typename T, int DP>
+__device__ __forceinline__ void mma_d(f32x4& acc, const T* Xn_tile, const OwnFrag<T, DP>& f, int l16, int g) {
+    using LY = Lay<T, DP>;
+    const T* p = Xn_tile + l16 * LY::PN + g * LY::VEC;
+#pragma unroll
+    for (int c = 0; c < LY::NC; ++c) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(p + c * LY::CW);
+        if constexpr (ET<T>::F32) {
+            const f32x4 af = __builtin_bit_cast(f32x4, a);
+            const f32x4 bf = __builtin_bit_cast(f32x4, f.v[c]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[e], bf[e], acc, 0, 0, 0);
+        } else {
+            acc = ET<T>::mma(a, f.v[c], acc);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// seq-contraction over one 32-row chunk: acc[t][m = d][n = own] += sum_x Xt[d][x] * P[x][own].
+// SeqB is the B operand built from the two accumulator tiles p0 (rows 0..15) and p1 (rows 16..31).
+// ---------------------------------------------------------------------------------------------------------------------
+
+template <typename T> struct SeqB {
+    u32x4 v;  // 8 values in k-slot order s = 4 h + r
+};
+template <> struct SeqB<float> {
+    f32x4 h0, h1;
+};
+
+template <typename T> __device__ __forceinline__ SeqB<T> make_seqb(f32x4 p0, f32x4 p1) {
+    SeqB<T> b;
+    if constexpr (ET<T>::F32) {
+        b.h0 = p0;
+        b.h1 = p1;
+    } else {
+        using V8 = typename ET<T>::v8;
+        V8 r;
+        r[0] = (T)p0[0];
+        r[1] = (T)p0[1];
+        r[2] = (T)p0[2];
+        r[3] = (T)p0[3];
+        r[4] = (T)p1[0];
+        r[5] = (T)p1[1];
+        r[6] = (T)p1[2];
+        r[7] = (T)p1[3];
+        b.v = __builtin_bit_cast(u32x4, r);
+    }
+    return b;
+}
+
+template <typename T> struct SeqA {
+    u32x4 v;
+};
+template <> struct SeqA<float> {
+    f32x4 h0, h1;
+};
+
+// A operand of d tile t: lane (d = 16 t + l16, group g).
+template <typename T, int DP> __device__ __forceinline__ SeqA<T> read_seqa(const T* Xt, int t, int l16, int g) {
+    using LY = Lay<T, DP>;
+    const T* p = Xt + (16 * t + l16) * LY::PT;
+    SeqA<T> a;
+    if constexpr (ET<T>::F32) {
+        a.h0 = *reinterpret_cast<const f32x4*>(p + 4 * g);
+        a.h1 = *reinterpret_cast<const f32x4*>(p + 16 + 4 * g);
+    } else {
+        a.v = *reinterpret_cast<const u32x4*>(p + 8 * g);
+    }
+    return a;
+}
+
+template <typename T> __device__ __forceinline__ f32x4 mma_seq(f32x4 acc, const SeqA<T>& a, const SeqB<T>& b) {
+    if constexpr (ET<T>::F32) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.h0[r], b.h0[r], acc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.h1[r], b.h1[r], acc, 0, 0, 0);
+        return acc;
+    } else {
+        return ET<T>::mma(a.v, b.v, acc);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// Cooperative staging of one other-side chunk (rows x0 .. x0 + CH - 1) into LDS, natural and/or transposed.
+// ---------------------------------------------------------------------------------------------------------------------
+
+template <typename T, int DP, bool NAT, bool TR>
+__device__ __forceinline__ void stage_chunk(T* Xn, T* Xt, const T* base, int64_t srow, int x0, int L, int D, int tid,
+                                            int nthr) {
+    using LY = Lay<T, DP>;
+    constexpr int VPR = DP / LY::VEC;  // 16-byte vectors per row
+    for (int it = tid; it < CH * VPR; it += nthr) {
+        const int x = it % CH;           // consecutive lanes take consecutive rows (conflict-free transposed writes)
+        const int c = it / CH;
+        const int row = x0 + x;
+        const int d0 = c * LY::VEC;
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (row < L && d0 < D) val = *reinterpret_cast<const u32x4*>(base + (int64_t)row * srow + d0);
+        if constexpr (NAT) *reinterpret_cast<u32x4*>(Xn + x * LY::PN + d0) = val;
+        if constexpr (TR) {
+            const int col = tr_col<T>(x);
+            if constexpr (ET<T>::F32) {
+                const f32x4 e = __builtin_bit_cast(f32x4, val);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) Xt[(d0 + j) * LY::PT + col] = e[j];
+            } else {
+                using V8 = typename ET<T>::v8;
+                const V8 e = __builtin_bit_cast(V8, val);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) Xt[(d0 + j) * LY::PT + col] = e[j];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// Row stores of seq-contraction outputs: lane (own, g) of tile t holds d = 16 t + 4 g + r.
+// ---------------------------------------------------------------------------------------------------------------------
+
+template <typename T> __device__ __forceinline__ void store4(T* p, f32x4 v) {
+    if constexpr (ET<T>::F32) {
+        *reinterpret_cast<f32x4*>(p) = v;
+    } else {
+        using V4 = typename ET<T>::v4;
+        V4 r;
+        r[0] = (T)v[0];
+        r[1] = (T)v[1];
+        r[2] = (T)v[2];
+        r[3] = (T)v[3];
+        *reinterpret_cast<u32x2*>(p) = __builtin_bit_cast(u32x2, r);
+    }
+}
+
+template <typename T> __device__ __forceinline__ f32x4 load4(const T* p) {
+    if constexpr (ET<T>::F32) {
+        return *reinterpret_cast<const f32x4*>(p);
+    } else {
+        using V4 = typename ET<T>::v4;
+        const V4 r = __builtin_bit_cast(V4, *reinterpret_cast<const u32x2*>(p));
+        return f32x4{(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
+    }
+}
+
+}  // namespace ebr

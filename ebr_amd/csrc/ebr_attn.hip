@@ -1,0 +1,864 @@
+// gfx950 kernels of the fused second-order attention path and their C ABI (include/ebr_attn.h).
+//
+// Algorithm (per (b, h) slice, s = scale):
+//   S = s Q K^T, lse = rowlogsumexp(S), P = exp(S - lse), O = P V                              (forward)
+//   dP = dO V^T, Dr = rowsum(dO * O), dS = P (dP - Dr), dQ = s dS K, dK = s dS^T Q, dV = P^T dO  (backward)
+//   A = s (gQ K^T + Q gK^T), Bm = dO gV^T, E = rowsum(P A), T = rowsum(dS A + P Bm),
+//   dS2 = dS A + P Bm - E dS - T P, Pa = P A - E P,
+//   hQ = s (dS2 K + dS gK), hK = s (dS2^T Q + dS^T gQ), hV = Pa^T dO, hdO = Pa V + P gV          (backward of backward)
+// following reference models/fused_attn/reference.py:32-91 (dense form) and the streaming row form of
+// models/fused_attn/triton_kernels.py:347-445 (hQ = s (X - E U - T Z), hdO = W - E O).
+//
+// Two passes over a slice, each a grid of 64-lane waves that own 16 rows and stream the other side in 32-row
+// LDS chunks (attn_tiles.hpp):
+//   row pass  own = queries: forward; dQ (+ Dr); hQ, hdO (+ Dr, E, T)
+//   col pass  own = keys:    dK, dV; hK, hV (reads lse, Dr, E, T of the query rows)
+// For L <= 128 one workgroup holds every row of a slice (one wave per 16 rows) and runs the row pass and then the
+// col pass, passing the row statistics through LDS: one launch, each input read once. Longer slices run the passes
+// as two launches that exchange the statistics through a caller-provided fp32 scratch.
+//
+// Precision (reference models/fused_attn/triton_kernels.py:15-17, 48-56, 84-90, 689-693): fp32 accumulation; for
+// 16-bit inputs the L x L tiles (P, dS, dS2, ...) are rounded to the input type before they enter an MFMA; exp is
+// exp2 of a small difference times log2(e); P = exp2(fma(qk, s, -lse) * log2(e)).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+
+#include "../../include/ebr_attn.h"
+#include "attn_tiles.hpp"
+
+namespace ebr {
+
+struct Strided {
+    const void* p;
+    int64_t sb, sh, sl;
+};
+
+struct Args {
+    int B, H, L, D;
+    float scale;
+    int nblk;       // own-row blocks per (b, h)
+    int xcd_remap;  // 1: keep the blocks of one (b, h) on one XCD
+    Strided q, k, v, dO, gq, gk, gv;
+    const void* o;      // contiguous [B, H, L, D]
+    const float* lse;   // contiguous [B, H, L]
+    void* out0;
+    void* out1;
+    void* out2;
+    void* out3;
+    float* lse_out;
+    float* stats;       // [3][B * H * L] fp32: Dr, E, T (two-launch shapes only)
+    int64_t bhl;        // B * H * L
+};
+
+template <typename T> __device__ __forceinline__ const T* slice(const Strided& t, int b, int h) {
+    return reinterpret_cast<const T*>(t.p) + (int64_t)b * t.sb + (int64_t)h * t.sh;
+}
+
+// Workgroup -> (bh, own block). Workgroups are dispatched round-robin over the 8 XCDs; with xcd_remap the blocks of
+// one (b, h), which read the same other-side rows, land on the same XCD and share its L2.
+__device__ __forceinline__ void decode_block(const Args& a, int& bh, int& blk) {
+    int i = blockIdx.x;
+    const int total = gridDim.x;
+    if (a.xcd_remap && (total & 7) == 0) {
+        const int per = total >> 3;
+        i = (i & 7) * per + (i >> 3);
+    }
+    bh = i / a.nblk;
+    blk = i - bh * a.nblk;
+}
+
+struct WaveIds {
+    int tid, nthr, wave, lane, l16, g;
+};
+
+__device__ __forceinline__ WaveIds wave_ids() {
+    WaveIds w;
+    w.tid = threadIdx.x;
+    w.nthr = blockDim.x;
+    w.wave = w.tid >> 6;
+    w.lane = w.tid & 63;
+    w.l16 = w.lane & 15;
+    w.g = w.lane >> 4;
+    return w;
+}
+
+// Writes rows of a transposed seq-contraction accumulator: lane (own, g) of tile t holds d = 16 t + 4 g + r.
+template <typename T, int DP>
+__device__ __forceinline__ void store_rows(void* out, int64_t row_off, const f32x4 (&acc)[DP / 16], float mul, int D,
+                                           int g) {
+    T* p = reinterpret_cast<T*>(out) + row_off;
+#pragma unroll
+    for (int t = 0; t < DP / 16; ++t) {
+        const int d = 16 * t + 4 * g;
+        if (d < D) store4<T>(p + d, acc[t] * mul);
+    }
+}
+
+// =====================================================================================================================
+// Forward (row pass): online softmax over 32-key chunks.
+// =====================================================================================================================
+
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd(Args a) {
+    using LY = Lay<T, DP>;
+    __shared__ __align__(16) unsigned char smem[LY::NATB + LY::TRB];
+    T* Kn = reinterpret_cast<T*>(smem);
+    T* Vt = reinterpret_cast<T*>(smem + LY::NATB);
+    const WaveIds w = wave_ids();
+    const int W = w.nthr >> 6;
+    int bh, blk;
+    decode_block(a, bh, blk);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L, D = a.D;
+    const int row0 = blk * 16 * W + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    const T* Q = slice<T>(a.q, b, h);
+    const T* K = slice<T>(a.k, b, h);
+    const T* V = slice<T>(a.v, b, h);
+
+    OwnFrag<T, DP> qf;
+    load_own<T, DP>(qf, Q, a.q.sl, own, L, D, w.g);
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 acc[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float sc = a.scale;
+
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        stage_chunk<T, DP, true, false>(Kn, nullptr, K, a.k.sl, x0, L, D, w.tid, w.nthr);
+        stage_chunk<T, DP, false, true>(nullptr, Vt, V, a.v.sl, x0, L, D, w.tid, w.nthr);
+        __syncthreads();
+        if (!active) continue;
+        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        mma_d<T, DP>(s0, Kn, qf, w.l16, w.g);
+        mma_d<T, DP>(s1, Kn + 16 * LY::PN, qf, w.l16, w.g);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int x = x0 + 4 * w.g + r;
+            s0[r] = (x < L) ? s0[r] * sc : -INFINITY;
+            s1[r] = (x + 16 < L) ? s1[r] * sc : -INFINITY;
+            mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+        }
+        const float mnew = fmaxf(m, xmax4(mx));
+        const float alpha = fast_exp2((m - mnew) * LOG2E);
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s0[r] = fast_exp2((s0[r] - mnew) * LOG2E);
+            s1[r] = fast_exp2((s1[r] - mnew) * LOG2E);
+            ps += s0[r] + s1[r];
+        }
+        lsum = lsum * alpha + ps;
+        const SeqB<T> pb = make_seqb<T>(s0, s1);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            const SeqA<T> va = read_seqa<T, DP>(Vt, t, w.l16, w.g);
+            acc[t] = mma_seq<T>(acc[t] * alpha, va, pb);
+        }
+        m = mnew;
+    }
+    if (!active) return;
+    lsum = xsum4(lsum);
+    if (own < L) {
+        const int64_t r = (int64_t)bh * L + own;
+        store_rows<T, DP>(a.out0, r * D, acc, 1.f / lsum, D, w.g);
+        if (w.g == 0) a.lse_out[r] = m + logf(lsum);
+    }
+}
+
+// =====================================================================================================================
+// Backward
+// =====================================================================================================================
+
+// Row pass: own = 16 query rows per wave; dQ = s sum_j dS[i][j] K[j]. Writes Dr (and lse) for the col pass:
+// FUSED -> LDS array st ([lse | Dr], STAT_MAX each, indexed by query row), else -> a.stats (Dr only).
+template <typename T, int DP, bool FUSED>
+__device__ __forceinline__ void bwd_row(const Args& a, int bh, int own_base, unsigned char* smem, float* st) {
+    using LY = Lay<T, DP>;
+    T* Kn = reinterpret_cast<T*>(smem);
+    T* Vn = reinterpret_cast<T*>(smem + LY::NATB);
+    T* Kt = reinterpret_cast<T*>(smem + 2 * LY::NATB);
+    const WaveIds w = wave_ids();
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L, D = a.D;
+    const int row0 = own_base + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    const T* K = slice<T>(a.k, b, h);
+    const T* V = slice<T>(a.v, b, h);
+    const float sc = a.scale;
+
+    OwnFrag<T, DP> qf, df, of;
+    load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, D, w.g);
+    load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, D, w.g);
+    load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * D, D, own, L, D, w.g);
+    const float dr = xsum4(frag_dot<T, DP>(df, of));
+    const float lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
+    if (w.g == 0 && active) {
+        if constexpr (FUSED) {
+            st[own] = (own < L) ? lse : INFINITY;
+            st[STAT_MAX + own] = (own < L) ? dr : 0.f;
+        } else {
+            if (own < L) a.stats[(int64_t)bh * L + own] = dr;
+        }
+    }
+
+    f32x4 acc[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        stage_chunk<T, DP, true, true>(Kn, Kt, K, a.k.sl, x0, L, D, w.tid, w.nthr);
+        stage_chunk<T, DP, true, false>(Vn, nullptr, V, a.v.sl, x0, L, D, w.tid, w.nthr);
+        __syncthreads();
+        if (!active) continue;
+        f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+        mma_d<T, DP>(p0, Kn, qf, w.l16, w.g);
+        mma_d<T, DP>(p1, Kn + 16 * LY::PN, qf, w.l16, w.g);
+        mma_d<T, DP>(d0, Vn, df, w.l16, w.g);
+        mma_d<T, DP>(d1, Vn + 16 * LY::PN, df, w.l16, w.g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int x = x0 + 4 * w.g + r;
+            p0[r] = (x < L) ? fast_exp2(fmaf(p0[r], sc, -lse) * LOG2E) : 0.f;
+            p1[r] = (x + 16 < L) ? fast_exp2(fmaf(p1[r], sc, -lse) * LOG2E) : 0.f;
+            d0[r] = p0[r] * (d0[r] - dr);
+            d1[r] = p1[r] * (d1[r] - dr);
+        }
+        const SeqB<T> dsb = make_seqb<T>(d0, d1);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], read_seqa<T, DP>(Kt, t, w.l16, w.g), dsb);
+    }
+    if (active && own < L) store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * D, acc, sc, D, w.g);
+}
+
+// Col pass: own = 16 key rows per wave; dK = s sum_i dS[i][j] Q[i], dV = sum_i P[i][j] dO[i].
+// FUSED -> row statistics from the LDS array st (full length); else staged per chunk from a.lse / a.stats.
+template <typename T, int DP, bool FUSED>
+__device__ __forceinline__ void bwd_col(const Args& a, int bh, int own_base, unsigned char* smem, const float* st) {
+    using LY = Lay<T, DP>;
+    T* Qn = reinterpret_cast<T*>(smem);
+    T* On = reinterpret_cast<T*>(smem + LY::NATB);  // dO natural
+    T* Qt = reinterpret_cast<T*>(smem + 2 * LY::NATB);
+    T* Ot = reinterpret_cast<T*>(smem + 2 * LY::NATB + LY::TRB);  // dO transposed
+    float* stc = reinterpret_cast<float*>(smem + 2 * LY::NATB + 2 * LY::TRB);
+    const WaveIds w = wave_ids();
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L, D = a.D;
+    const int row0 = own_base + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    const T* Q = slice<T>(a.q, b, h);
+    const T* dO = slice<T>(a.dO, b, h);
+    const float sc = a.scale;
+
+    OwnFrag<T, DP> kf, vf;
+    load_own<T, DP>(kf, slice<T>(a.k, b, h), a.k.sl, own, L, D, w.g);
+    load_own<T, DP>(vf, slice<T>(a.v, b, h), a.v.sl, own, L, D, w.g);
+    f32x4 ak[LY::NT], av[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        stage_chunk<T, DP, true, true>(Qn, Qt, Q, a.q.sl, x0, L, D, w.tid, w.nthr);
+        stage_chunk<T, DP, true, true>(On, Ot, dO, a.dO.sl, x0, L, D, w.tid, w.nthr);
+        if constexpr (!FUSED) {
+            for (int i = w.tid; i < CH; i += w.nthr) {
+                const int x = x0 + i;
+                const int64_t r = (int64_t)bh * L + x;
+                stc[i] = (x < L) ? a.lse[r] : INFINITY;
+                stc[CH + i] = (x < L) ? a.stats[r] : 0.f;
+            }
+        }
+        __syncthreads();
+        if (!active) continue;
+        const float* sl = FUSED ? st + x0 : stc;
+        const float* sd = FUSED ? st + STAT_MAX + x0 : stc + CH;
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(sl + 4 * w.g);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(sl + 16 + 4 * w.g);
+        const f32x4 r0 = *reinterpret_cast<const f32x4*>(sd + 4 * w.g);
+        const f32x4 r1 = *reinterpret_cast<const f32x4*>(sd + 16 + 4 * w.g);
+        f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+        mma_d<T, DP>(p0, Qn, kf, w.l16, w.g);
+        mma_d<T, DP>(p1, Qn + 16 * LY::PN, kf, w.l16, w.g);
+        mma_d<T, DP>(d0, On, vf, w.l16, w.g);
+        mma_d<T, DP>(d1, On + 16 * LY::PN, vf, w.l16, w.g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p0[r] = fast_exp2(fmaf(p0[r], sc, -l0[r]) * LOG2E);  // lse = +inf on padded rows -> P = 0
+            p1[r] = fast_exp2(fmaf(p1[r], sc, -l1[r]) * LOG2E);
+            d0[r] = p0[r] * (d0[r] - r0[r]);
+            d1[r] = p1[r] * (d1[r] - r1[r]);
+        }
+        const SeqB<T> pb = make_seqb<T>(p0, p1);
+        const SeqB<T> dsb = make_seqb<T>(d0, d1);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            av[t] = mma_seq<T>(av[t], read_seqa<T, DP>(Ot, t, w.l16, w.g), pb);
+            ak[t] = mma_seq<T>(ak[t], read_seqa<T, DP>(Qt, t, w.l16, w.g), dsb);
+        }
+    }
+    if (active && own < L) {
+        const int64_t r = ((int64_t)bh * L + own) * D;
+        store_rows<T, DP>(a.out1, r, ak, sc, D, w.g);
+        store_rows<T, DP>(a.out2, r, av, 1.f, D, w.g);
+    }
+}
+
+template <typename T, int DP> struct BwdSmem {
+    using LY = Lay<T, DP>;
+    static constexpr int ROW = 2 * LY::NATB + LY::TRB;
+    static constexpr int COL = 2 * LY::NATB + 2 * LY::TRB + 2 * CH * 4;
+    static constexpr int PASS = ROW > COL ? ROW : COL;
+};
+
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_fused(Args a) {
+    __shared__ __align__(16) unsigned char smem[BwdSmem<T, DP>::PASS];
+    __shared__ __align__(16) float st[2 * STAT_MAX];
+    for (int i = threadIdx.x; i < STAT_MAX; i += blockDim.x) {
+        st[i] = INFINITY;
+        st[STAT_MAX + i] = 0.f;
+    }
+    __syncthreads();
+    const int bh = blockIdx.x;
+    bwd_row<T, DP, true>(a, bh, 0, smem, st);
+    bwd_col<T, DP, true>(a, bh, 0, smem, st);
+}
+
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_row(Args a) {
+    __shared__ __align__(16) unsigned char smem[BwdSmem<T, DP>::ROW];
+    int bh, blk;
+    decode_block(a, bh, blk);
+    bwd_row<T, DP, false>(a, bh, blk * (int)blockDim.x / 4, smem, nullptr);
+}
+
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_col(Args a) {
+    __shared__ __align__(16) unsigned char smem[BwdSmem<T, DP>::COL];
+    int bh, blk;
+    decode_block(a, bh, blk);
+    bwd_col<T, DP, false>(a, bh, blk * (int)blockDim.x / 4, smem, nullptr);
+}
+
+// =====================================================================================================================
+// Backward of the backward
+// =====================================================================================================================
+
+// Row pass: own = 16 query rows per wave, streaming form (E and T are known only at the end of the row):
+//   X = sum_j (dS A + P Bm) K + dS gK,  U = dS K,  Z = P K,  W = (P A) V + P gV,
+//   hQ = s (X - E U - T Z),  hdO = W - E O.
+// Writes lse, Dr, E, T of its rows: FUSED -> LDS st ([lse | Dr | E | T]), else -> a.stats ([Dr | E | T]).
+template <typename T, int DP, bool FUSED>
+__device__ __forceinline__ void bb_row(const Args& a, int bh, int own_base, unsigned char* smem, float* st) {
+    using LY = Lay<T, DP>;
+    T* Kn = reinterpret_cast<T*>(smem);
+    T* gKn = reinterpret_cast<T*>(smem + LY::NATB);
+    T* Vn = reinterpret_cast<T*>(smem + 2 * LY::NATB);
+    T* gVn = reinterpret_cast<T*>(smem + 3 * LY::NATB);
+    T* Kt = reinterpret_cast<T*>(smem + 4 * LY::NATB);
+    T* gKt = reinterpret_cast<T*>(smem + 4 * LY::NATB + LY::TRB);
+    T* Vt = reinterpret_cast<T*>(smem + 4 * LY::NATB + 2 * LY::TRB);
+    T* gVt = reinterpret_cast<T*>(smem + 4 * LY::NATB + 3 * LY::TRB);
+    const WaveIds w = wave_ids();
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L, D = a.D;
+    const int row0 = own_base + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    const T* K = slice<T>(a.k, b, h);
+    const T* gK = slice<T>(a.gk, b, h);
+    const T* V = slice<T>(a.v, b, h);
+    const T* gV = slice<T>(a.gv, b, h);
+    const T* O = reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * D;
+    const float sc = a.scale;
+
+    OwnFrag<T, DP> qf, gqf, df, of;
+    load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, D, w.g);
+    load_own<T, DP>(gqf, slice<T>(a.gq, b, h), a.gq.sl, own, L, D, w.g);
+    load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, D, w.g);
+    load_own<T, DP>(of, O, D, own, L, D, w.g);
+    const float dr = xsum4(frag_dot<T, DP>(df, of));
+    const float lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
+
+    f32x4 X[LY::NT], U[LY::NT], Z[LY::NT], Wv[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) X[t] = U[t] = Z[t] = Wv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float e_acc = 0.f, t_acc = 0.f;
+
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        stage_chunk<T, DP, true, true>(Kn, Kt, K, a.k.sl, x0, L, D, w.tid, w.nthr);
+        stage_chunk<T, DP, true, true>(gKn, gKt, gK, a.gk.sl, x0, L, D, w.tid, w.nthr);
+        stage_chunk<T, DP, true, true>(Vn, Vt, V, a.v.sl, x0, L, D, w.tid, w.nthr);
+        stage_chunk<T, DP, true, true>(gVn, gVt, gV, a.gv.sl, x0, L, D, w.tid, w.nthr);
+        __syncthreads();
+        if (!active) continue;
+        f32x4 p[2], dp[2], at[2], bm[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int off = hh * 16 * LY::PN;
+            mma_d<T, DP>(p[hh], Kn + off, qf, w.l16, w.g);
+            mma_d<T, DP>(dp[hh], Vn + off, df, w.l16, w.g);
+            mma_d<T, DP>(at[hh], Kn + off, gqf, w.l16, w.g);
+            mma_d<T, DP>(at[hh], gKn + off, qf, w.l16, w.g);
+            mma_d<T, DP>(bm[hh], gVn + off, df, w.l16, w.g);
+        }
+        f32x4 ds[2], pa[2], m1[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int x = x0 + 16 * hh + 4 * w.g + r;
+                const float pv = (x < L) ? fast_exp2(fmaf(p[hh][r], sc, -lse) * LOG2E) : 0.f;
+                const float dsv = pv * (dp[hh][r] - dr);
+                const float av = at[hh][r] * sc;
+                p[hh][r] = pv;
+                ds[hh][r] = dsv;
+                pa[hh][r] = pv * av;
+                m1[hh][r] = fmaf(dsv, av, pv * bm[hh][r]);
+                e_acc += pa[hh][r];
+                t_acc += m1[hh][r];
+            }
+        }
+        const SeqB<T> pb = make_seqb<T>(p[0], p[1]);
+        const SeqB<T> dsb = make_seqb<T>(ds[0], ds[1]);
+        const SeqB<T> pab = make_seqb<T>(pa[0], pa[1]);
+        const SeqB<T> m1b = make_seqb<T>(m1[0], m1[1]);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            const SeqA<T> ka = read_seqa<T, DP>(Kt, t, w.l16, w.g);
+            X[t] = mma_seq<T>(X[t], ka, m1b);
+            U[t] = mma_seq<T>(U[t], ka, dsb);
+            Z[t] = mma_seq<T>(Z[t], ka, pb);
+            X[t] = mma_seq<T>(X[t], read_seqa<T, DP>(gKt, t, w.l16, w.g), dsb);
+            Wv[t] = mma_seq<T>(Wv[t], read_seqa<T, DP>(Vt, t, w.l16, w.g), pab);
+            Wv[t] = mma_seq<T>(Wv[t], read_seqa<T, DP>(gVt, t, w.l16, w.g), pb);
+        }
+    }
+    const float E = xsum4(e_acc);
+    const float Tm = xsum4(t_acc);
+    if (active && own < L) {
+        const int64_t r = ((int64_t)bh * L + own) * D;
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            const int d = 16 * t + 4 * w.g;
+            if (d < D) {
+                const f32x4 hq = (X[t] - E * U[t] - Tm * Z[t]) * sc;
+                const f32x4 hdo = Wv[t] - E * load4<T>(O + (int64_t)own * D + d);
+                store4<T>(reinterpret_cast<T*>(a.out0) + r + d, hq);
+                store4<T>(reinterpret_cast<T*>(a.out3) + r + d, hdo);
+            }
+        }
+    }
+    if (w.g == 0 && active) {
+        if constexpr (FUSED) {
+            const bool ok = own < L;
+            st[own] = ok ? lse : INFINITY;
+            st[STAT_MAX + own] = ok ? dr : 0.f;
+            st[2 * STAT_MAX + own] = ok ? E : 0.f;
+            st[3 * STAT_MAX + own] = ok ? Tm : 0.f;
+        } else if (own < L) {
+            const int64_t r = (int64_t)bh * L + own;
+            a.stats[r] = dr;
+            a.stats[a.bhl + r] = E;
+            a.stats[2 * a.bhl + r] = Tm;
+        }
+    }
+}
+
+// Col pass: own = 16 key rows per wave; hK = s sum_i (dS2[i][j] Q[i] + dS[i][j] gQ[i]), hV = sum_i Pa[i][j] dO[i].
+template <typename T, int DP, bool FUSED>
+__device__ __forceinline__ void bb_col(const Args& a, int bh, int own_base, unsigned char* smem, const float* st) {
+    using LY = Lay<T, DP>;
+    T* Qn = reinterpret_cast<T*>(smem);
+    T* gQn = reinterpret_cast<T*>(smem + LY::NATB);
+    T* On = reinterpret_cast<T*>(smem + 2 * LY::NATB);  // dO natural
+    T* Qt = reinterpret_cast<T*>(smem + 3 * LY::NATB);
+    T* gQt = reinterpret_cast<T*>(smem + 3 * LY::NATB + LY::TRB);
+    T* Ot = reinterpret_cast<T*>(smem + 3 * LY::NATB + 2 * LY::TRB);  // dO transposed
+    float* stc = reinterpret_cast<float*>(smem + 3 * LY::NATB + 3 * LY::TRB);
+    const WaveIds w = wave_ids();
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L, D = a.D;
+    const int row0 = own_base + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    const T* Q = slice<T>(a.q, b, h);
+    const T* gQ = slice<T>(a.gq, b, h);
+    const T* dO = slice<T>(a.dO, b, h);
+    const float sc = a.scale;
+
+    OwnFrag<T, DP> kf, gkf, vf, gvf;
+    load_own<T, DP>(kf, slice<T>(a.k, b, h), a.k.sl, own, L, D, w.g);
+    load_own<T, DP>(gkf, slice<T>(a.gk, b, h), a.gk.sl, own, L, D, w.g);
+    load_own<T, DP>(vf, slice<T>(a.v, b, h), a.v.sl, own, L, D, w.g);
+    load_own<T, DP>(gvf, slice<T>(a.gv, b, h), a.gv.sl, own, L, D, w.g);
+    f32x4 hk[LY::NT], hv[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        stage_chunk<T, DP, true, true>(Qn, Qt, Q, a.q.sl, x0, L, D, w.tid, w.nthr);
+        stage_chunk<T, DP, true, true>(gQn, gQt, gQ, a.gq.sl, x0, L, D, w.tid, w.nthr);
+        stage_chunk<T, DP, true, true>(On, Ot, dO, a.dO.sl, x0, L, D, w.tid, w.nthr);
+        if constexpr (!FUSED) {
+            for (int i = w.tid; i < CH; i += w.nthr) {
+                const int x = x0 + i;
+                const int64_t r = (int64_t)bh * L + x;
+                const bool ok = x < L;
+                stc[i] = ok ? a.lse[r] : INFINITY;
+                stc[CH + i] = ok ? a.stats[r] : 0.f;
+                stc[2 * CH + i] = ok ? a.stats[a.bhl + r] : 0.f;
+                stc[3 * CH + i] = ok ? a.stats[2 * a.bhl + r] : 0.f;
+            }
+        }
+        __syncthreads();
+        if (!active) continue;
+        const int sstride = FUSED ? STAT_MAX : CH;
+        const float* s_base = FUSED ? st + x0 : stc;
+        f32x4 p[2], dp[2], at[2], bm[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int off = hh * 16 * LY::PN;
+            mma_d<T, DP>(p[hh], Qn + off, kf, w.l16, w.g);
+            mma_d<T, DP>(dp[hh], On + off, vf, w.l16, w.g);
+            mma_d<T, DP>(at[hh], gQn + off, kf, w.l16, w.g);
+            mma_d<T, DP>(at[hh], Qn + off, gkf, w.l16, w.g);
+            mma_d<T, DP>(bm[hh], On + off, gvf, w.l16, w.g);
+        }
+        f32x4 ds[2], ds2[2], pa[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int so = 16 * hh + 4 * w.g;
+            const f32x4 ls = *reinterpret_cast<const f32x4*>(s_base + so);
+            const f32x4 rs = *reinterpret_cast<const f32x4*>(s_base + sstride + so);
+            const f32x4 es = *reinterpret_cast<const f32x4*>(s_base + 2 * sstride + so);
+            const f32x4 ts = *reinterpret_cast<const f32x4*>(s_base + 3 * sstride + so);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pv = fast_exp2(fmaf(p[hh][r], sc, -ls[r]) * LOG2E);
+                const float dsv = pv * (dp[hh][r] - rs[r]);
+                const float av = at[hh][r] * sc;
+                p[hh][r] = pv;
+                ds[hh][r] = dsv;
+                const float m1 = fmaf(dsv, av, pv * bm[hh][r]);
+                ds2[hh][r] = m1 - es[r] * dsv - ts[r] * pv;
+                pa[hh][r] = pv * (av - es[r]);
+            }
+        }
+        const SeqB<T> dsb = make_seqb<T>(ds[0], ds[1]);
+        const SeqB<T> ds2b = make_seqb<T>(ds2[0], ds2[1]);
+        const SeqB<T> pab = make_seqb<T>(pa[0], pa[1]);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            hk[t] = mma_seq<T>(hk[t], read_seqa<T, DP>(Qt, t, w.l16, w.g), ds2b);
+            hk[t] = mma_seq<T>(hk[t], read_seqa<T, DP>(gQt, t, w.l16, w.g), dsb);
+            hv[t] = mma_seq<T>(hv[t], read_seqa<T, DP>(Ot, t, w.l16, w.g), pab);
+        }
+    }
+    if (active && own < L) {
+        const int64_t r = ((int64_t)bh * L + own) * D;
+        store_rows<T, DP>(a.out1, r, hk, sc, D, w.g);
+        store_rows<T, DP>(a.out2, r, hv, 1.f, D, w.g);
+    }
+}
+
+template <typename T, int DP> struct BbSmem {
+    using LY = Lay<T, DP>;
+    static constexpr int ROW = 4 * LY::NATB + 4 * LY::TRB;
+    static constexpr int COL = 3 * LY::NATB + 3 * LY::TRB + 4 * CH * 4;
+    static constexpr int PASS = ROW > COL ? ROW : COL;
+};
+
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_fused(Args a) {
+    __shared__ __align__(16) unsigned char smem[BbSmem<T, DP>::PASS];
+    __shared__ __align__(16) float st[4 * STAT_MAX];
+    for (int i = threadIdx.x; i < STAT_MAX; i += blockDim.x) {
+        st[i] = INFINITY;
+        st[STAT_MAX + i] = 0.f;
+        st[2 * STAT_MAX + i] = 0.f;
+        st[3 * STAT_MAX + i] = 0.f;
+    }
+    __syncthreads();
+    const int bh = blockIdx.x;
+    bb_row<T, DP, true>(a, bh, 0, smem, st);
+    bb_col<T, DP, true>(a, bh, 0, smem, st);
+}
+
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_row(Args a) {
+    __shared__ __align__(16) unsigned char smem[BbSmem<T, DP>::ROW];
+    int bh, blk;
+    decode_block(a, bh, blk);
+    bb_row<T, DP, false>(a, bh, blk * (int)blockDim.x / 4, smem, nullptr);
+}
+
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_col(Args a) {
+    __shared__ __align__(16) unsigned char smem[BbSmem<T, DP>::COL];
+    int bh, blk;
+    decode_block(a, bh, blk);
+    bb_col<T, DP, false>(a, bh, blk * (int)blockDim.x / 4, smem, nullptr);
+}
+
+// =====================================================================================================================
+// Host side: argument checks, plan, launch.
+// =====================================================================================================================
+
+constexpr int STREAM_WAVES = 4;  // waves (x16 own rows) per workgroup of the two-launch kernels
+
+static bool fused_shape(int L) { return L <= STAT_MAX; }
+
+static int elem_size(int dtype) { return dtype == EBR_DTYPE_F32 ? 4 : 2; }
+
+static int check_shape(int dtype, int B, int H, int L, int D) {
+    if (dtype != EBR_DTYPE_F32 && dtype != EBR_DTYPE_BF16 && dtype != EBR_DTYPE_F16) return EBR_ERR_DTYPE;
+    if (B < 1 || H < 1 || L < 1 || D < 1 || D > 128) return EBR_ERR_SHAPE;
+    const int vec = dtype == EBR_DTYPE_F32 ? 4 : 8;
+    if (D % vec) return EBR_ERR_SHAPE;
+    if ((int64_t)B * H * L >= ((int64_t)1 << 31)) return EBR_ERR_SHAPE;
+    return EBR_OK;
+}
+
+static int check_ptr(const void* p, int es, bool need) {
+    if (!p) return need ? EBR_ERR_NULL : EBR_OK;
+    return ((uintptr_t)p % 16) ? EBR_ERR_ALIGN : EBR_OK;
+}
+
+static int check_strided(const void* p, const int64_t* s, int es) {
+    int rc = check_ptr(p, es, true);
+    if (rc) return rc;
+    if (!s) return EBR_ERR_NULL;
+    for (int i = 0; i < 3; ++i)
+        if (s[i] < 0 || ((s[i] * es) % 16)) return EBR_ERR_ALIGN;
+    return EBR_OK;
+}
+
+static Strided mk(const void* p, const int64_t* s) {
+    Strided t;
+    t.p = p;
+    t.sb = s ? s[0] : 0;
+    t.sh = s ? s[1] : 0;
+    t.sl = s ? s[2] : 0;
+    return t;
+}
+
+static int launch_rc() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? EBR_OK : EBR_ERR_HIP_BASE + (int)e;
+}
+
+template <template <typename, int> class F, typename... Rest>
+static int dispatch(int dtype, int D, Rest&&... rest) {
+    if (dtype == EBR_DTYPE_F32) {
+        if (D <= 16) return F<float, 16>::run(rest...);
+        if (D <= 32) return F<float, 32>::run(rest...);
+        if (D <= 64) return F<float, 64>::run(rest...);
+        return F<float, 128>::run(rest...);
+    }
+    if (dtype == EBR_DTYPE_BF16) {
+        if (D <= 32) return F<__bf16, 32>::run(rest...);
+        if (D <= 64) return F<__bf16, 64>::run(rest...);
+        return F<__bf16, 128>::run(rest...);
+    }
+    if (D <= 32) return F<_Float16, 32>::run(rest...);
+    if (D <= 64) return F<_Float16, 64>::run(rest...);
+    return F<_Float16, 128>::run(rest...);
+}
+
+static void plan_stream(Args& a, int64_t bh, int& grid, int& threads) {
+    a.nblk = (a.L + 16 * STREAM_WAVES - 1) / (16 * STREAM_WAVES);
+    a.xcd_remap = 1;
+    grid = (int)(bh * a.nblk);
+    threads = 64 * STREAM_WAVES;
+}
+
+template <typename T, int DP> struct FwdLaunch {
+    static int run(Args a, hipStream_t s) {
+        const int64_t bh = (int64_t)a.B * a.H;
+        int grid, threads;
+        if (fused_shape(a.L)) {
+            a.nblk = 1;
+            a.xcd_remap = 0;
+            grid = (int)bh;
+            threads = 64 * ((a.L + 15) / 16);
+        } else {
+            plan_stream(a, bh, grid, threads);
+        }
+        hipLaunchKernelGGL((k_fwd<T, DP>), dim3(grid), dim3(threads), 0, s, a);
+        return launch_rc();
+    }
+};
+
+template <typename T, int DP> struct BwdLaunch {
+    static int run(Args a, hipStream_t s) {
+        const int64_t bh = (int64_t)a.B * a.H;
+        if (fused_shape(a.L)) {
+            a.nblk = 1;
+            a.xcd_remap = 0;
+            hipLaunchKernelGGL((k_bwd_fused<T, DP>), dim3((int)bh), dim3(64 * ((a.L + 15) / 16)), 0, s, a);
+            return launch_rc();
+        }
+        int grid, threads;
+        plan_stream(a, bh, grid, threads);
+        hipLaunchKernelGGL((k_bwd_row<T, DP>), dim3(grid), dim3(threads), 0, s, a);
+        int rc = launch_rc();
+        if (rc) return rc;
+        hipLaunchKernelGGL((k_bwd_col<T, DP>), dim3(grid), dim3(threads), 0, s, a);
+        return launch_rc();
+    }
+};
+
+template <typename T, int DP> struct BbLaunch {
+    static int run(Args a, hipStream_t s) {
+        const int64_t bh = (int64_t)a.B * a.H;
+        if (fused_shape(a.L)) {
+            a.nblk = 1;
+            a.xcd_remap = 0;
+            hipLaunchKernelGGL((k_bb_fused<T, DP>), dim3((int)bh), dim3(64 * ((a.L + 15) / 16)), 0, s, a);
+            return launch_rc();
+        }
+        int grid, threads;
+        plan_stream(a, bh, grid, threads);
+        hipLaunchKernelGGL((k_bb_row<T, DP>), dim3(grid), dim3(threads), 0, s, a);
+        int rc = launch_rc();
+        if (rc) return rc;
+        hipLaunchKernelGGL((k_bb_col<T, DP>), dim3(grid), dim3(threads), 0, s, a);
+        return launch_rc();
+    }
+};
+
+static Args base_args(int B, int H, int L, int D, float scale) {
+    Args a = {};
+    a.B = B;
+    a.H = H;
+    a.L = L;
+    a.D = D;
+    a.scale = scale;
+    a.bhl = (int64_t)B * H * L;
+    return a;
+}
+
+}  // namespace ebr
+
+using namespace ebr;
+
+extern "C" {
+
+int ebr_attn_abi_version(void) { return EBR_ATTN_ABI_VERSION; }
+
+const char* ebr_attn_arch(void) { return "gfx950"; }
+
+const char* ebr_attn_error_string(int code) {
+    switch (code) {
+        case EBR_OK: return "ok";
+        case EBR_ERR_DTYPE: return "unsupported dtype (expected fp32, bf16 or fp16)";
+        case EBR_ERR_SHAPE:
+            return "unsupported shape (need B, H, L >= 1, B*H*L < 2^31, D <= 128 and a multiple of 8 for 16-bit "
+                   "or 4 for fp32)";
+        case EBR_ERR_ALIGN: return "row start not 16-byte aligned (base pointer or a B/H/L stride)";
+        case EBR_ERR_NULL: return "required pointer is NULL";
+        case EBR_ERR_SCRATCH: return "scratch buffer required for this shape but NULL";
+        default: break;
+    }
+    if (code >= EBR_ERR_HIP_BASE) return hipGetErrorString((hipError_t)(code - EBR_ERR_HIP_BASE));
+    return "unknown error code";
+}
+
+int64_t ebr_attn_scratch_bytes(int op, int B, int H, int L, int D) {
+    (void)D;
+    if (B < 1 || H < 1 || L < 1) return 0;
+    if (fused_shape(L)) return 0;
+    const int64_t bhl = (int64_t)B * H * L;
+    if (op == EBR_OP_BWD) return bhl * 4;
+    if (op == EBR_OP_BWD_BWD) return 3 * bhl * 4;
+    return 0;
+}
+
+int ebr_attn_fwd(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
+                 const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], void* o, float* lse,
+                 void* stream) {
+    int rc = check_shape(dtype, B, H, L, D);
+    if (rc) return rc;
+    const int es = elem_size(dtype);
+    if ((rc = check_strided(q, q_str, es)) || (rc = check_strided(k, k_str, es)) ||
+        (rc = check_strided(v, v_str, es)) || (rc = check_ptr(o, es, true)) || (rc = check_ptr(lse, 4, true)))
+        return rc;
+    Args a = base_args(B, H, L, D, scale);
+    a.q = mk(q, q_str);
+    a.k = mk(k, k_str);
+    a.v = mk(v, v_str);
+    a.out0 = o;
+    a.lse_out = lse;
+    return dispatch<FwdLaunch>(dtype, D, a, (hipStream_t)stream);
+}
+
+int ebr_attn_bwd(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
+                 const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], const void* o,
+                 const float* lse, const void* dO, const int64_t dO_str[3], void* dq, void* dk, void* dv,
+                 float* scratch, void* stream) {
+    int rc = check_shape(dtype, B, H, L, D);
+    if (rc) return rc;
+    const int es = elem_size(dtype);
+    if ((rc = check_strided(q, q_str, es)) || (rc = check_strided(k, k_str, es)) ||
+        (rc = check_strided(v, v_str, es)) || (rc = check_strided(dO, dO_str, es)) ||
+        (rc = check_ptr(o, es, true)) || (rc = check_ptr(lse, 4, true)) || (rc = check_ptr(dq, es, true)) ||
+        (rc = check_ptr(dk, es, true)) || (rc = check_ptr(dv, es, true)))
+        return rc;
+    if (ebr_attn_scratch_bytes(EBR_OP_BWD, B, H, L, D) > 0 && !scratch) return EBR_ERR_SCRATCH;
+    Args a = base_args(B, H, L, D, scale);
+    a.q = mk(q, q_str);
+    a.k = mk(k, k_str);
+    a.v = mk(v, v_str);
+    a.dO = mk(dO, dO_str);
+    a.o = o;
+    a.lse = lse;
+    a.out0 = dq;
+    a.out1 = dk;
+    a.out2 = dv;
+    a.stats = scratch;
+    return dispatch<BwdLaunch>(dtype, D, a, (hipStream_t)stream);
+}
+
+int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
+                     const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], const void* o,
+                     const float* lse, const void* dO, const int64_t dO_str[3], const void* gq,
+                     const int64_t gq_str[3], const void* gk, const int64_t gk_str[3], const void* gv,
+                     const int64_t gv_str[3], void* hq, void* hk, void* hv, void* hdo, float* scratch,
+                     void* stream) {
+    int rc = check_shape(dtype, B, H, L, D);
+    if (rc) return rc;
+    const int es = elem_size(dtype);
+    if ((rc = check_strided(q, q_str, es)) || (rc = check_strided(k, k_str, es)) ||
+        (rc = check_strided(v, v_str, es)) || (rc = check_strided(dO, dO_str, es)) ||
+        (rc = check_strided(gq, gq_str, es)) || (rc = check_strided(gk, gk_str, es)) ||
+        (rc = check_strided(gv, gv_str, es)) || (rc = check_ptr(o, es, true)) || (rc = check_ptr(lse, 4, true)) ||
+        (rc = check_ptr(hq, es, true)) || (rc = check_ptr(hk, es, true)) || (rc = check_ptr(hv, es, true)) ||
+        (rc = check_ptr(hdo, es, true)))
+        return rc;
+    if (ebr_attn_scratch_bytes(EBR_OP_BWD_BWD, B, H, L, D) > 0 && !scratch) return EBR_ERR_SCRATCH;
+    Args a = base_args(B, H, L, D, scale);
+    a.q = mk(q, q_str);
+    a.k = mk(k, k_str);
+    a.v = mk(v, v_str);
+    a.dO = mk(dO, dO_str);
+    a.gq = mk(gq, gq_str);
+    a.gk = mk(gk, gk_str);
+    a.gv = mk(gv, gv_str);
+    a.o = o;
+    a.lse = lse;
+    a.out0 = hq;
+    a.out1 = hk;
+    a.out2 = hv;
+    a.out3 = hdo;
+    a.stats = scratch;
+    return dispatch<BbLaunch>(dtype, D, a, (hipStream_t)stream);
+}
+
+}  // extern "C"

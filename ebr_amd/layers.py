@@ -1,0 +1,127 @@
+"""Layers of the energy network (the attention path's callers): fp32-weight linear layers cast at use, rms_norm,
+SwiGLU and 2D rotary position embeddings.
+
+Behaviour follows reference ``models/layers.py``: ``trunc_normal_init_`` (:16-34, truncated normal rescaled to the
+requested std), ``rms_norm`` (:37-42, fp32 statistics, input dtype out), ``CastedLinear`` (:45-57, fp32 weights with
+std 1/sqrt(fan_in), cast to the input dtype), ``SwiGLU`` (:74-84, intermediate round(2/3 * expansion * hidden) rounded
+up to a multiple of 256) and the broadcast 2D RoPE (:93-143: first half of each head rotates with the cell's row,
+second half with its column).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+RMS_NORM_EPS = 1e-5
+ROPE_THETA = 10000.0
+
+
+def trunc_normal_init_(tensor: torch.Tensor, std: float = 1.0, lower: float = -2.0, upper: float = 2.0) -> torch.Tensor:
+    """In place: normal truncated to [lower, upper] standard units, scaled so the truncated law has std ``std``."""
+    with torch.no_grad():
+        if std == 0:
+            return tensor.zero_()
+        # Inverse-CDF sampling of the truncated standard normal, then a variance correction for the truncation.
+        cdf_lo = 0.5 * (1.0 + math.erf(lower / math.sqrt(2.0)))
+        cdf_hi = 0.5 * (1.0 + math.erf(upper / math.sqrt(2.0)))
+        phi = lambda x: math.exp(-0.5 * x * x) / math.sqrt(2.0 * math.pi)  # noqa: E731
+        mass = cdf_hi - cdf_lo
+        var = 1.0 + (lower * phi(lower) - upper * phi(upper)) / mass - ((phi(lower) - phi(upper)) / mass) ** 2
+        scale = std / math.sqrt(var)
+        tensor.uniform_(2.0 * cdf_lo - 1.0, 2.0 * cdf_hi - 1.0)
+        tensor.erfinv_().mul_(math.sqrt(2.0) * scale)
+        return tensor.clamp_(lower * scale, upper * scale)
+
+
+def rms_norm(x: torch.Tensor, variance_epsilon: float) -> torch.Tensor:
+    """Unit RMS over the last dim, statistics in fp32, result in the input dtype."""
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + variance_epsilon)).to(x.dtype)
+
+
+class CastedLinear(nn.Module):
+    """y = x W^T (+ b) with fp32 parameters cast to x.dtype at every call."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool) -> None:
+        super().__init__()
+        w = torch.empty(out_features, in_features)
+        self.weight = nn.Parameter(trunc_normal_init_(w, std=in_features**-0.5))
+        self.bias = nn.Parameter(torch.zeros(out_features)) if bias else None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        b = None if self.bias is None else self.bias.to(x.dtype)
+        return F.linear(x, self.weight.to(x.dtype), b)
+
+
+def swiglu_intermediate(hidden_size: int, expansion: float) -> int:
+    n = round(expansion * hidden_size * 2 / 3)
+    return ((n + 255) // 256) * 256
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, hidden_size: int, expansion: float) -> None:
+        super().__init__()
+        inter = swiglu_intermediate(hidden_size, expansion)
+        self.gate_up_proj = CastedLinear(hidden_size, 2 * inter, bias=False)
+        self.down_proj = CastedLinear(inter, hidden_size, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gate, up = self.gate_up_proj(x).chunk(2, dim=-1)
+        return self.down_proj(F.silu(gate) * up)
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+class RotaryEmbedding2D(nn.Module):
+    """cos/sin tables for a ``height x width`` board: rows for the first half of D, columns for the second."""
+
+    def __init__(self, dim: int, height: int, width: int, base: float = ROPE_THETA) -> None:
+        super().__init__()
+        half = dim // 2
+        inv = base ** (-torch.arange(0, half, 2, dtype=torch.float32) / half)
+        ang_h = torch.arange(height, dtype=torch.float32)[:, None] * inv[None, :]
+        ang_w = torch.arange(width, dtype=torch.float32)[:, None] * inv[None, :]
+        ang_h, ang_w = ang_h.repeat(1, 2), ang_w.repeat(1, 2)
+        self.register_buffer("cos_h", ang_h.cos(), persistent=False)
+        self.register_buffer("sin_h", ang_h.sin(), persistent=False)
+        self.register_buffer("cos_w", ang_w.cos(), persistent=False)
+        self.register_buffer("sin_w", ang_w.sin(), persistent=False)
+
+    def forward(self):
+        return (self.cos_h, self.cos_w), (self.sin_h, self.sin_w)
+
+
+def apply_rope(cos_sin, q: torch.Tensor, k: torch.Tensor):
+    """2D RoPE on q, k of shape [B, N, heads, D] with N = height * width (row-major cells)."""
+    (cos_h, cos_w), (sin_h, sin_w) = cos_sin
+    hgt, wid = cos_h.shape[0], cos_w.shape[0]
+
+    def rot(x: torch.Tensor) -> torch.Tensor:
+        b, n, nh, d = x.shape
+        xg = x.reshape(b, hgt, wid, nh, d).to(cos_h.dtype)
+        r, c = xg[..., : d // 2], xg[..., d // 2 :]
+        r = r * cos_h[None, :, None, None, :] + rotate_half(r) * sin_h[None, :, None, None, :]
+        c = c * cos_w[None, None, :, None, :] + rotate_half(c) * sin_w[None, None, :, None, :]
+        return torch.cat((r, c), dim=-1).to(x.dtype).reshape(b, n, nh, d)
+
+    return rot(q), rot(k)
+
+
+__all__ = [
+    "RMS_NORM_EPS",
+    "CastedLinear",
+    "RotaryEmbedding2D",
+    "SwiGLU",
+    "apply_rope",
+    "rms_norm",
+    "rotate_half",
+    "swiglu_intermediate",
+    "trunc_normal_init_",
+]

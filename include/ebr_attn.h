@@ -1,0 +1,109 @@
+/* C ABI of the MI355X (gfx950) fused second-order attention library, libebr_attn.so.
+ *
+ * Non-causal softmax attention on [B, H, L, D] tensors: the forward, its backward and the backward of the
+ * backward. Each entry replaces one op of the reference's fused path and takes the same arguments in the same
+ * meaning; only the calling convention is C (plain pointers, sizes and strides, no framework types).
+ *
+ * Conventions shared by every entry point:
+ *   - dtype: EBR_DTYPE_F32, EBR_DTYPE_BF16 or EBR_DTYPE_F16; all tensor arguments of one call share it, except
+ *     lse and the scratch, which are always fp32.
+ *   - Strided inputs pass their element strides for the B, H and L dimensions as int64_t[3]; the D dimension is
+ *     unit-stride. A stride may be 0 (an expanded row, e.g. an all-zero cotangent). Every row start must be 16-byte
+ *     aligned: base pointer 16-byte aligned and each stride a multiple of 16 bytes.
+ *   - o, lse and every output are contiguous [B, H, L, D] (lse: [B, H, L], fp32, natural log).
+ *   - scale is the softmax scale (D ** -0.5 by default), already rounded to fp32.
+ *   - stream is a hipStream_t (NULL = the null stream). Kernels are enqueued on it; nothing synchronises.
+ *   - The caller owns every buffer; the library allocates nothing and keeps no pointer after returning.
+ *   - Return value: 0 on success, otherwise an EBR_ERR_* code or EBR_ERR_HIP_BASE + hipError_t;
+ *     ebr_attn_error_string() describes it. Argument checks run before anything is enqueued.
+ *   - Supported shapes: B, H, L >= 1; D a multiple of 8 (16-bit) or 4 (fp32) with D <= 128.
+ */
+#ifndef EBR_ATTN_H
+#define EBR_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EBR_ATTN_ABI_VERSION 1
+
+enum {
+    EBR_DTYPE_F32 = 0,
+    EBR_DTYPE_BF16 = 1,
+    EBR_DTYPE_F16 = 2,
+};
+
+enum {
+    EBR_OK = 0,
+    EBR_ERR_DTYPE = 1,       /* dtype code not supported (the reference raises TypeError) */
+    EBR_ERR_SHAPE = 2,       /* B, H, L or D outside the supported range (the reference raises ValueError) */
+    EBR_ERR_ALIGN = 3,       /* a pointer or stride breaks the 16-byte row alignment rule */
+    EBR_ERR_NULL = 4,        /* a required pointer is NULL */
+    EBR_ERR_SCRATCH = 5,     /* scratch is NULL but this shape needs one (see ebr_attn_scratch_bytes) */
+    EBR_ERR_HIP_BASE = 1000, /* EBR_ERR_HIP_BASE + hipError_t of a failed launch */
+};
+
+enum {
+    EBR_OP_FWD = 0,
+    EBR_OP_BWD = 1,
+    EBR_OP_BWD_BWD = 2,
+};
+
+/* Forward: o = softmax(scale * q k^T) v and lse = row logsumexp of scale * q k^T.
+ * Replaces ebr_fused::attn_fwd(q, k, v, scale) -> (o, lse)
+ *   (reference models/fused_attn/ops.py:65-77; Triton launcher models/fused_attn/triton_kernels.py:696-728). */
+int ebr_attn_fwd(int dtype, int B, int H, int L, int D, float scale,
+                 const void* q, const int64_t q_str[3],
+                 const void* k, const int64_t k_str[3],
+                 const void* v, const int64_t v_str[3],
+                 void* o, float* lse, void* stream);
+
+/* Backward: (dq, dk, dv) = gradient of <dO, o> with respect to (q, k, v); rowsum(dO * o) uses the stored o.
+ * Replaces ebr_fused::attn_bwd(q, k, v, o, lse, do, scale) -> (dq, dk, dv)
+ *   (reference models/fused_attn/ops.py:80-95; Triton launcher models/fused_attn/triton_kernels.py:731-839).
+ * scratch: fp32, ebr_attn_scratch_bytes(EBR_OP_BWD, ...) bytes; may be NULL when that size is 0. */
+int ebr_attn_bwd(int dtype, int B, int H, int L, int D, float scale,
+                 const void* q, const int64_t q_str[3],
+                 const void* k, const int64_t k_str[3],
+                 const void* v, const int64_t v_str[3],
+                 const void* o, const float* lse,
+                 const void* dO, const int64_t dO_str[3],
+                 void* dq, void* dk, void* dv, float* scratch, void* stream);
+
+/* Backward of the backward: (hq, hk, hv, hdo) = derivative of <gq, dq> + <gk, dk> + <gv, dv> with respect to
+ * (q, k, v, dO). The reference op also takes dq, which it does not read; this entry omits it.
+ * Replaces ebr_fused::attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale) -> (hq, hk, hv, hdo)
+ *   (reference models/fused_attn/ops.py:98-121; Triton launcher models/fused_attn/triton_kernels.py:842-968).
+ * scratch: fp32, ebr_attn_scratch_bytes(EBR_OP_BWD_BWD, ...) bytes; may be NULL when that size is 0. */
+int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale,
+                     const void* q, const int64_t q_str[3],
+                     const void* k, const int64_t k_str[3],
+                     const void* v, const int64_t v_str[3],
+                     const void* o, const float* lse,
+                     const void* dO, const int64_t dO_str[3],
+                     const void* gq, const int64_t gq_str[3],
+                     const void* gk, const int64_t gk_str[3],
+                     const void* gv, const int64_t gv_str[3],
+                     void* hq, void* hk, void* hv, void* hdo, float* scratch, void* stream);
+
+/* Bytes of fp32 scratch an op needs for this shape (0 when the shape runs in one workgroup per (b, h)).
+ * No reference counterpart: the Triton launchers allocate their row-statistics buffers themselves
+ *   (models/fused_attn/triton_kernels.py:679-686, 910-912); here the caller does. */
+int64_t ebr_attn_scratch_bytes(int op, int B, int H, int L, int D);
+
+/* Text for a return code. No reference counterpart (Python exceptions carry the message there). */
+const char* ebr_attn_error_string(int code);
+
+/* EBR_ATTN_ABI_VERSION of the loaded library. No reference counterpart. */
+int ebr_attn_abi_version(void);
+
+/* Offload architecture the library was built for, e.g. "gfx950". No reference counterpart. */
+const char* ebr_attn_arch(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EBR_ATTN_H */

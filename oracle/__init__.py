@@ -1,0 +1,33 @@
+"""CPU oracle for the fused second-order attention path.
+
+TEST INFRASTRUCTURE ONLY. Nothing in the shipped package (``ebr_amd``) imports this package. It may be imported by
+``tests/``, by ``__graft_entry__.smoke()`` (as the checker of one small GPU call) and by ``bench.py``'s
+``cpu_baseline`` leg (timed as the host-CPU eager path). It is never the implementation under measurement.
+
+Contents:
+- ``attention_ref``: dense restatement of the reference's eager attention and of its three fused ops
+  (``models/fused_attn/reference.py``, ``models/attention.py:49-54``), plus the autograd recipes that pin them.
+
+Pinning (each function has at least one check that does not retype its formula):
+- ``attn_fwd``: ``torch.softmax``/``torch.logsumexp`` closed forms and known answers (L = 1, Q = 0, row shift,
+  key/value permutation) in ``tests/test_oracle.py``.
+- ``attn_bwd``: the VJP of ``math_attention`` through torch autograd, fp64 ``gradcheck`` on tiny shapes, linearity in
+  dO and the identity rowsum(dO*O) = rowsum(P*dP).
+- ``attn_bwd_bwd``: the double backward of ``math_attention`` through torch autograd (create_graph), fp64
+  ``gradgradcheck``, a central finite-difference Hessian-vector check, linearity in (gQ, gK, gV) and the
+  zero-cotangent special cases.
+- ``math_attention``: ``torch.nn.functional.scaled_dot_product_attention`` (fp64) and the known answers above.
+No function is left "parity unpinned".
+"""
+
+from oracle.attention_ref import (  # noqa: F401
+    attn_bwd,
+    attn_bwd_bwd,
+    attn_fwd,
+    autograd_bwd,
+    autograd_bwd_bwd,
+    default_scale,
+    make_inputs,
+    math_attention,
+    rel_err,
+)

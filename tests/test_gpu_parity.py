@@ -1,0 +1,276 @@
+"""GPU parity: the gfx950 kernels (through the C ABI, via the ebr_fused ops) against the CPU oracle.
+
+Bars: max|a - ref| / max|ref| <= 1e-5 for fp32 and <= 2e-2 for bf16/fp16, for O, lse, dQ, dK,
+dV and hQ, hK, hV, hdO, on identical seeded inputs. Slices (b, h) are independent, so at the full BASELINE sizes a
+random sample of slices is checked against the oracle run on exactly those slices.
+"""
+
+import math
+
+import pytest
+import torch
+
+import oracle
+from ebr_amd.fused_attn import ops  # noqa: F401  (registers torch.ops.ebr_fused.*)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def _say(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+
+
+def _inputs(B, H, L, D, dtype, seed=0):
+    scale = 0.125 if dtype != torch.float32 else None
+    return oracle.make_inputs(B, H, L, D, dtype=dtype, seed=seed, qkv_scale=scale)
+
+
+def _hip_all(q, k, v, do, gq, gk, gv, scale, dev):
+    """All three ops on the GPU; returns CPU tensors (o, lse, dq, dk, dv, hq, hk, hv, hdo)."""
+    t = [x.to(dev) for x in (q, k, v, do, gq, gk, gv)]
+    qd, kd, vd, dod, gqd, gkd, gvd = t
+    o, lse = torch.ops.ebr_fused.attn_fwd(qd, kd, vd, scale)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(qd, kd, vd, o, lse, dod, scale)
+    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(qd, kd, vd, o, lse, dod, dq, gqd, gkd, gvd, scale)
+    torch.cuda.synchronize()
+    return [x.cpu() for x in (o, lse, dq, dk, dv, hq, hk, hv, hdo)]
+
+
+def _oracle_all(q, k, v, do, gq, gk, gv, scale, o=None, lse=None, chunk=None):
+    """Oracle outputs. bwd and bwd_bwd consume the given (o, lse) when provided (the GPU forward's), so each phase
+    is checked on its own inputs, as the reference's ops are."""
+    o_ref, lse_ref = oracle.attn_fwd(q, k, v, scale, chunk=chunk)
+    o_in = o_ref if o is None else o
+    lse_in = lse_ref if lse is None else lse
+    dq, dk, dv = oracle.attn_bwd(q, k, v, o_in, lse_in, do, scale, chunk=chunk)
+    hq, hk, hv, hdo = oracle.attn_bwd_bwd(q, k, v, o_in, lse_in, do, dq, gq, gk, gv, scale, chunk=chunk)
+    return [o_ref, lse_ref, dq, dk, dv, hq, hk, hv, hdo]
+
+
+NAMES = ["o", "lse", "dq", "dk", "dv", "hq", "hk", "hv", "hdo"]
+
+
+def _compare(got, ref, dtype, label, tol=None):
+    tol = TOL[dtype] if tol is None else tol
+    errs = {n: oracle.rel_err(g, r) for n, g, r in zip(NAMES, got, ref)}
+    for n, g in zip(NAMES, got):
+        assert torch.isfinite(g.float()).all(), f"{label}: non-finite {n}"
+    bad = {n: e for n, e in errs.items() if not (e <= tol)}
+    print(f"{label}: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    assert not bad, f"{label}: over tolerance {tol}: {bad}"
+    return errs
+
+
+def _case(B, H, L, D, dtype, dev, seed=0, tol=None):
+    label = f"B={B} H={H} L={L} D={D} {str(dtype).split('.')[-1]} seed={seed}"
+    _say(label)
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, dtype, seed)
+    scale = D**-0.5
+    got = _hip_all(q, k, v, do, gq, gk, gv, scale, dev)
+    ref = _oracle_all(q, k, v, do, gq, gk, gv, scale, o=got[0], lse=got[1])
+    if L == 1:
+        # Known answer: with one key P = 1, so O = V, dV = dO, hdO = gV, and dQ, dK, hQ, hK, hV are exactly 0; their
+        # reference values are rounding noise, so they are checked against the size of the non-zero outputs.
+        tol_ = TOL[dtype] if tol is None else tol
+        zero = {"dq", "dk", "hq", "hk", "hv"}
+        big = max(float(got[NAMES.index(n)].abs().max()) for n in ("dv", "hdo"))
+        for n, g_ in zip(NAMES, got):
+            if n in zero:
+                assert float(g_.abs().max()) <= tol_ * big, f"{label}: {n} not ~0"
+        keep = [i for i, n in enumerate(NAMES) if n not in zero]
+        got = [got[i] if i in keep else torch.zeros(1) for i in range(len(NAMES))]
+        ref = [ref[i] if i in keep else torch.zeros(1) for i in range(len(NAMES))]
+        assert torch.equal(got[0].float(), v.float()), "L=1: O must equal V"
+    return _compare(got, ref, dtype, label, tol)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# Shape sweep: one-workgroup kernels (L <= 128) and two-launch kernels (L > 128), every head dim, every dtype.
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("L", [1, 7, 16, 17, 31, 32, 33, 64, 81, 100, 127, 128])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_small_L(cuda, L, dtype):
+    _case(2, 3, L, 64, dtype, cuda, seed=L)
+
+
+@pytest.mark.parametrize("L", [129, 200, 333])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_long_L(cuda, L, dtype):
+    _case(2, 2, L, 64, dtype, cuda, seed=L)
+
+
+@pytest.mark.parametrize("D", [16, 32, 48, 128])
+@pytest.mark.parametrize("L", [45, 150])
+def test_head_dims_fp32(cuda, D, L):
+    _case(2, 2, L, D, torch.float32, cuda, seed=D + L)
+
+
+@pytest.mark.parametrize("D", [32, 40, 128])
+@pytest.mark.parametrize("L", [45, 150])
+def test_head_dims_bf16(cuda, D, L):
+    _case(2, 2, L, D, torch.bfloat16, cuda, seed=D + L)
+
+
+@pytest.mark.parametrize("L", [81, 200])
+def test_fp16(cuda, L):
+    _case(2, 2, L, 64, torch.float16, cuda, seed=5)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# BASELINE configurations
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+def test_config0_nqueens_fp32_full(cuda):
+    """Config 0: fp32 B=32 H=8 L=64 D=64, Q/K/V/dO/R ~ N(0,1) seed 0, every slice, 1e-5."""
+    _case(32, 8, 64, 64, torch.float32, cuda, seed=0)
+
+
+def _sampled(B, H, L, D, dtype, dev, nsample, seed=0):
+    label = f"sampled B={B} H={H} L={L} D={D} {str(dtype).split('.')[-1]}"
+    _say(label)
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, dtype, seed)
+    scale = D**-0.5
+    got = _hip_all(q, k, v, do, gq, gk, gv, scale, dev)
+    g = torch.Generator().manual_seed(1234)
+    idx = torch.randperm(B * H, generator=g)[:nsample]
+
+    def pick(t):
+        return t.reshape(B * H, *t.shape[2:])[idx].unsqueeze(0)
+
+    sub = [pick(t) for t in (q, k, v, do, gq, gk, gv)]
+    got_s = [pick(t) for t in got]
+    ref = _oracle_all(*sub, scale, o=got_s[0], lse=got_s[1])
+    return _compare(got_s, ref, dtype, label)
+
+
+def test_config1_sudoku_bf16_full_size(cuda):
+    """Config 1: bf16 B=768 H=8 L=81 D=64 at full size; 128 random slices checked."""
+    _sampled(768, 8, 81, 64, torch.bfloat16, cuda, 128)
+
+
+def test_config2_maze_bf16_full_size(cuda):
+    """Config 2: bf16 B=64 H=8 L=900 D=64 at full size; 12 random slices checked."""
+    _sampled(64, 8, 900, 64, torch.bfloat16, cuda, 12)
+
+
+def test_config4_shape_bf16(cuda):
+    """Config 4's attention shape (L=100) on a reduced batch; all slices checked."""
+    _case(40, 8, 100, 64, torch.bfloat16, cuda, seed=4)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# Strided inputs, stride-0 cotangents, the autograd path
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+def test_strided_views(cuda):
+    """q, k, v as transposed views of one [B, L, 3, H, D] projection (non-contiguous B/H/L strides)."""
+    B, H, L, D = 3, 4, 81, 64
+    _say("strided qkv views")
+    g = torch.Generator().manual_seed(7)
+    qkv = (torch.randn(B, L, 3, H, D, generator=g) * 0.125).to(torch.bfloat16)
+    do = torch.randn(B, H, L, D, generator=g).to(torch.bfloat16)
+    gq, gk, gv = (torch.randn(B, H, L, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    qkv_d = qkv.to(cuda)
+    q, k, v = (qkv_d[:, :, i].transpose(1, 2) for i in range(3))
+    assert not q.is_contiguous()
+    scale = D**-0.5
+    o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do.to(cuda), scale)
+    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(
+        q, k, v, o, lse, do.to(cuda), dq, gq.to(cuda), gk.to(cuda), gv.to(cuda), scale
+    )
+    got = [x.cpu() for x in (o, lse, dq, dk, dv, hq, hk, hv, hdo)]
+    qc, kc, vc = (qkv[:, :, i].transpose(1, 2).contiguous() for i in range(3))
+    ref = _oracle_all(qc, kc, vc, do, gq, gk, gv, scale, o=got[0], lse=got[1])
+    _compare(got, ref, torch.bfloat16, "strided")
+
+
+@pytest.mark.parametrize("L", [81, 200])
+def test_zero_cotangent_rows(cuda, L):
+    """gq = gk = 0 as stride-0 expanded rows: hV = 0 and hdO = P gV exactly as the dense formula gives."""
+    B, H, D = 2, 2, 64
+    dtype = torch.float32
+    _say(f"stride-0 cotangents L={L}")
+    q, k, v, do, _, _, gv = _inputs(B, H, L, D, dtype, 3)
+    scale = D**-0.5
+    z = torch.zeros(D, dtype=dtype).expand(B, H, L, D)
+    dev = cuda
+    qd, kd, vd, dod = (t.to(dev) for t in (q, k, v, do))
+    zd = torch.zeros(D, device=dev, dtype=dtype).expand(B, H, L, D)
+    o, lse = torch.ops.ebr_fused.attn_fwd(qd, kd, vd, scale)
+    dq, _, _ = torch.ops.ebr_fused.attn_bwd(qd, kd, vd, o, lse, dod, scale)
+    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(qd, kd, vd, o, lse, dod, dq, zd, zd, gv.to(dev), scale)
+    ref = oracle.attn_bwd_bwd(q, k, v, o.cpu(), lse.cpu(), do, None, z, z, gv, scale)
+    assert hv.abs().max().item() == 0.0
+    for n, g_, r in zip(["hq", "hk", "hv", "hdo"], (hq, hk, hv, hdo), ref):
+        if n != "hv":
+            assert oracle.rel_err(g_.cpu(), r) <= 1e-5, n
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_autograd_double_backward(cuda, dtype):
+    """fused_attention + autograd.grad(create_graph) + second grad, against autograd on the eager math attention."""
+    from ebr_amd.fused_attn import fused_attention
+
+    B, H, L, D = 2, 4, 81, 64
+    _say(f"autograd double backward {dtype}")
+    q, k, v, do, r1, r2, r3 = _inputs(B, H, L, D, dtype, 11)
+    ref = oracle.autograd_bwd_bwd(q, k, v, do, r1, r2, r3)
+    ref_first = oracle.autograd_bwd(q, k, v, do)
+    qd, kd, vd = (t.to(cuda).requires_grad_(True) for t in (q, k, v))
+    dod = do.to(cuda).requires_grad_(True)
+    out = fused_attention(qd, kd, vd)
+    dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), dod, create_graph=True)
+    phi = (dq * r1.to(cuda)).sum() + (dk * r2.to(cuda)).sum() + (dv * r3.to(cuda)).sum()
+    hq, hk, hv, hdo = torch.autograd.grad(phi, (qd, kd, vd, dod))
+    tol = TOL[dtype]
+    for n, g_, r in zip(["dq", "dk", "dv"], (dq, dk, dv), ref_first):
+        assert oracle.rel_err(g_.detach().cpu(), r) <= tol, n
+    for n, g_, r in zip(["hq", "hk", "hv", "hdo"], (hq, hk, hv, hdo), ref):
+        e = oracle.rel_err(g_.cpu(), r)
+        print(f"  {n} rel={e:.2e}", flush=True)
+        assert e <= tol, n
+
+
+def test_verify_second_order_fused(cuda):
+    """The reference's runtime gate (b=2, seq=32, heads=2, head_dim=16, fp32, rtol 5e-2) passes on the HIP backend."""
+    from ebr_amd.attention import get_backend, verify_second_order
+
+    _say("verify_second_order(fused)")
+    verify_second_order(get_backend("fused"), device=cuda)
+
+
+def test_outputs_do_not_depend_on_stale_memory(cuda):
+    """Two calls with the same inputs after a caching-allocator churn give bit-identical results (no reads of
+    uninitialised memory, no run-to-run nondeterminism)."""
+    B, H, L, D = 4, 4, 150, 64
+    _say("determinism")
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, torch.bfloat16, 21)
+    scale = D**-0.5
+    a = _hip_all(q, k, v, do, gq, gk, gv, scale, cuda)
+    junk = torch.full((64 << 20,), float("nan"), device=cuda)
+    del junk
+    b = _hip_all(q, k, v, do, gq, gk, gv, scale, cuda)
+    for n, x, y in zip(NAMES, a, b):
+        assert torch.equal(x, y), n
+
+
+def test_bad_arguments_raise(cuda):
+    _say("argument errors")
+    q = torch.randn(2, 2, 16, 64, device=cuda)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.attn_fwd(q, q[:, :, :8], q, 0.125)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.attn_fwd(q, q.half(), q, 0.125)
+    with pytest.raises(TypeError):
+        torch.ops.ebr_fused.attn_fwd(q.double(), q.double(), q.double(), 0.125)
+    with pytest.raises(ValueError):  # D > 128
+        x = torch.randn(1, 1, 4, 136, device=cuda)
+        torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
+    assert math.isfinite(1.0)
