@@ -1,0 +1,340 @@
+"""Benchmark of the gfx950 fused second-order attention (BASELINE metric: attention fwd + bwd + bwd_bwd TFLOP/s and %
+of the bf16 MFMA peak, on one GPU).
+
+A step is one pass of the hot path over one batch: attn_fwd -> attn_bwd -> attn_bwd_bwd through the ebr_fused ops
+(the calls an EBR graded microstep makes), on synthetic inputs of the BASELINE configuration already resident in HBM.
+Default workload: config 1 (Sudoku, bf16, B=768 H=8 L=81 D=64). Prints one JSON line.
+
+Timing: W untimed warm-up steps, then K steps bracketed by torch.cuda.synchronize(), timed with HIP events on the
+stream the kernels run on (torch's current stream). Steps rotate over several input sets (> the 256 MB MALL) so no
+step reads inputs the previous one left in the last-level cache. The dominant kernel (the backward of the backward)
+is also timed alone through the C ABI with preallocated outputs, for the roofline entry.
+
+cpu_baseline: the CPU oracle (the build's restatement of the reference's eager path) timed on this host's cores on a
+bounded sample of the same workload, reported in the same unit.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+from ebr_amd import _capi, roofline  # noqa: E402
+
+METRIC = "attn fwd+bwd+2bwd TFLOP/s & % bf16 MFMA peak; EBR train steps/sec (1 GPU)"
+
+CONFIGS = {
+    0: dict(name="nqueens8_attn_fp32", B=32, H=8, L=64, D=64, dtype=torch.float32, qkv_scale=None),
+    1: dict(name="sudoku_attn_bf16", B=768, H=8, L=81, D=64, dtype=torch.bfloat16, qkv_scale=0.125),
+    2: dict(name="maze_attn_bf16", B=64, H=8, L=900, D=64, dtype=torch.bfloat16, qkv_scale=0.125),
+}
+DT_NAME = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}
+DT_CODE = {torch.float32: _capi.DTYPE_F32, torch.bfloat16: _capi.DTYPE_BF16, torch.float16: _capi.DTYPE_F16}
+PHASES = ("fwd", "bwd", "bwd_bwd")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_sets(cfg: dict, dev: torch.device, nsets: int):
+    """Input set 0 follows the seeded recipe (CPU generator, seed 0: Q, K, V, dO, R1, R2, R3); further sets, only
+    there to defeat cache reuse between steps, are drawn on the GPU."""
+    import oracle  # test infrastructure: the seeded input recipe
+
+    B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
+    sets = [tuple(t.to(dev) for t in oracle.make_inputs(B, H, L, D, dtype=dt, seed=0, qkv_scale=cfg["qkv_scale"]))]
+    g = torch.Generator(device=dev).manual_seed(1)
+    for _ in range(1, nsets):
+        ts = [torch.randn((B, H, L, D), generator=g, device=dev) for _ in range(7)]
+        if cfg["qkv_scale"]:
+            ts[:3] = [t * cfg["qkv_scale"] for t in ts[:3]]
+        sets.append(tuple(t.to(dt) for t in ts))
+    return sets
+
+
+def step(inp, scale):
+    q, k, v, do, gq, gk, gv = inp
+    o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
+    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
+    return o, lse, dq
+
+
+def time_steps(sets, scale, steps: int, warmup: int):
+    """Whole-step time and per-phase event times (ms) over ``steps`` steps."""
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    for i in range(warmup):
+        step(sets[i % len(sets)], scale)
+    torch.cuda.synchronize()
+    marks = [[ev() for _ in range(4)] for _ in range(steps)]
+    t0, t1 = ev(), ev()
+    t0.record()
+    for i in range(steps):
+        q, k, v, do, gq, gk, gv = sets[i % len(sets)]
+        m = marks[i]
+        m[0].record()
+        o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+        m[1].record()
+        dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
+        m[2].record()
+        torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
+        m[3].record()
+    t1.record()
+    torch.cuda.synchronize()
+    total = t0.elapsed_time(t1)
+    phase = {p: sum(m[j].elapsed_time(m[j + 1]) for m in marks) / steps for j, p in enumerate(PHASES)}
+    return total / steps, phase
+
+
+def time_kernel_bwd_bwd(cfg, sets, scale, reps: int):
+    """Average duration (ms) of one ebr_attn_bwd_bwd launch through the C ABI, outputs preallocated, launched
+    back-to-back on torch's current stream over rotating input sets; HIP events on that stream."""
+    lib = _capi.load()
+    B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
+    dev = sets[0][0].device
+    prepared = []
+    for inp in sets:
+        q, k, v, do, gq, gk, gv = inp
+        o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+        outs = [torch.empty_like(q) for _ in range(4)]
+        prepared.append((inp, o, lse, outs))
+    nbytes = int(lib.ebr_attn_scratch_bytes(_capi.OP_BWD_BWD, B, H, L, D))
+    scratch = torch.empty(max(1, nbytes // 4), device=dev, dtype=torch.float32) if nbytes else None
+    sp = scratch.data_ptr() if scratch is not None else 0
+    stream = torch.cuda.current_stream(dev)
+    s3 = _capi.strides3
+
+    def launch(i):
+        (q, k, v, do, gq, gk, gv), o, lse, outs = prepared[i % len(prepared)]
+        rc = lib.ebr_attn_bwd_bwd(
+            DT_CODE[dt], B, H, L, D, ctypes.c_float(scale),
+            q.data_ptr(), s3(q), k.data_ptr(), s3(k), v.data_ptr(), s3(v), o.data_ptr(), lse.data_ptr(),
+            do.data_ptr(), s3(do), gq.data_ptr(), s3(gq), gk.data_ptr(), s3(gk), gv.data_ptr(), s3(gv),
+            outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(), outs[3].data_ptr(), sp,
+            ctypes.c_void_p(stream.cuda_stream),
+        )  # fmt: skip
+        _capi.check(rc, "ebr_attn_bwd_bwd")
+
+    for i in range(3):
+        launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def spot_check(cfg, sets, scale, nslices: int = 16) -> float:
+    """Max relative error of one step on input set 0 against the CPU oracle on a few (b, h) slices."""
+    import oracle
+
+    q, k, v, do, gq, gk, gv = sets[0]
+    o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
+    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
+    B, H = cfg["B"], cfg["H"]
+    idx = torch.arange(0, B * H, max(1, (B * H) // nslices))[:nslices]
+
+    def pick(t):
+        return t.detach().reshape(B * H, *t.shape[2:])[idx.to(t.device)].unsqueeze(0).cpu()
+
+    ins = [pick(t) for t in (q, k, v, do, gq, gk, gv)]
+    got = [pick(t) for t in (o, lse, dq, dk, dv, hq, hk, hv, hdo)]
+    o_r, lse_r = oracle.attn_fwd(ins[0], ins[1], ins[2], scale)
+    d_r = oracle.attn_bwd(ins[0], ins[1], ins[2], got[0], got[1], ins[3], scale)
+    h_r = oracle.attn_bwd_bwd(ins[0], ins[1], ins[2], got[0], got[1], ins[3], None, *ins[4:], scale)
+    return max(oracle.rel_err(g, r) for g, r in zip(got, [o_r, lse_r, *d_r, *h_r]))
+
+
+def cpu_baseline(cfg, scale, budget_s: float):
+    """The CPU oracle (eager dense path) on the first ``nbh`` (b, h) slices of the workload; fwd + bwd + bwd_bwd
+    timed together, median of 3 after one warm-up; nbh chosen so one pass takes about budget_s / 4."""
+    import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
+
+    def inputs(nbh):
+        bb = max(1, nbh // H)
+        return oracle.make_inputs(bb, H, L, D, dtype=dt, seed=0, qkv_scale=cfg["qkv_scale"]), bb
+
+    chunk = max(1, (1 << 22) // (L * L))  # (b, h) slices per dense pass: bounds the L x L temporaries
+
+    def one(inp):
+        q, k, v, do, gq, gk, gv = inp
+        o, lse = oracle.attn_fwd(q, k, v, scale, chunk=chunk)
+        dq, dk, dv = oracle.attn_bwd(q, k, v, o, lse, do, scale, chunk=chunk)
+        oracle.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale, chunk=chunk)
+
+    target = budget_s / 4.0
+    nbh = min(B * H, 64 * H)
+    while True:
+        inp, bb = inputs(nbh)
+        t = time.perf_counter()
+        one(inp)  # also the warm-up of the final size
+        probe = time.perf_counter() - t
+        if bb * H >= B * H or probe >= target / 2:
+            break
+        nbh = int(min(B * H, nbh * max(2.0, target / max(probe, 1e-3))))
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        one(inp)
+        times.append(time.perf_counter() - t)
+    sec = statistics.median(times)
+    flops = sum(roofline.phase_flops(p, bb, H, L, D) for p in PHASES)
+    return {
+        "value": round(flops / sec / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"CPU oracle (eager dense restatement of models/fused_attn/reference.py), fwd+bwd+bwd_bwd on "
+        f"{bb * H} of {B * H} (b,h) slices (B={bb}, H={H}, L={L}, D={D}, {DT_NAME[dt]} inputs, fp32 compute), "
+        f"median of 3 passes of {sec:.3f} s after 1 warm-up, torch threads={cores}",
+        "seconds_per_pass": round(sec, 4),
+        "cpu_model": _cpu_model(),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
+    ap.add_argument("--sets", type=int, default=3, help="input sets rotated across steps")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work (0 = skip)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+            "attention slices shard over (b, h) with no exchange, so N GPUs would each run this same workload",
+            file=sys.stderr,
+        )
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    _capi.load()
+    import ebr_amd.fused_attn.ops  # noqa: F401
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
+    scale = D**-0.5
+    es = torch.tensor([], dtype=dt).element_size()
+    dname = DT_NAME[dt]
+    log(f"workload {cfg['name']} B={B} H={H} L={L} D={D} {dname}; {args.sets} input sets")
+    sets = make_sets(cfg, dev, args.sets)
+
+    err = spot_check(cfg, sets, scale)
+    log(f"spot-check max rel err vs CPU oracle on 16 slices: {err:.3e}")
+
+    torch.cuda.synchronize()
+    ms_step, phase_ms = time_steps(sets, scale, args.steps, args.warmup)
+    log(f"ms/step {ms_step:.4f}; phases " + " ".join(f"{p}={phase_ms[p]:.4f}ms" for p in PHASES))
+    k_ms = time_kernel_bwd_bwd(cfg, sets, scale, args.kernel_reps)
+    log(f"bwd_bwd kernel (C ABI, back-to-back) {k_ms:.4f} ms")
+
+    flops_step = sum(roofline.phase_flops(p, B, H, L, D) for p in PHASES)
+    tflops = flops_step / (ms_step * 1e-3) / 1e12
+    peak = roofline.peak_tflops(dname)
+    t_roof = sum(roofline.roof_time_s(p, B, H, L, D, es, dname) for p in PHASES)
+    phases = {}
+    for p in PHASES:
+        f = roofline.phase_flops(p, B, H, L, D)
+        by = roofline.phase_bytes(p, B, H, L, D, es)
+        t = phase_ms[p] * 1e-3
+        phases[p] = {
+            "ms": round(phase_ms[p], 4),
+            "tflops": round(f / t / 1e12, 2),
+            "pct_bf16_peak": round(100 * f / t / 1e12 / roofline.PEAK_BF16_TFLOPS, 2),
+            "gbs": round(by / t / 1e9, 1),
+            "pct_roofline": round(100 * roofline.roof_time_s(p, B, H, L, D, es, dname) / t, 1),
+        }
+
+    hbm_bound = roofline.phase_bytes("bwd_bwd", B, H, L, D, es) / (roofline.PEAK_HBM_GBS * 1e9) >= roofline.phase_flops(
+        "bwd_bwd", B, H, L, D
+    ) / (peak * 1e12)
+    if hbm_bound:
+        achieved = roofline.phase_bytes("bwd_bwd", B, H, L, D, es) / (k_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": roofline.PEAK_HBM_GBS, "unit": "GB/s"}
+    else:
+        achieved = roofline.phase_flops("bwd_bwd", B, H, L, D) / (k_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = None
+    roof["kernel"] = "ebr_attn_bwd_bwd (k_bb_fused)" if L <= 128 else "ebr_attn_bwd_bwd (k_bb_row + k_bb_col)"
+    roof["kernel_ms"] = round(k_ms, 4)
+
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dname,
+        "data": "synthetic (seeded N(0,1) inputs; Q,K,V x 1/sqrt(64) for bf16 configs)",
+        "config": {
+            "workload": f"{cfg['name']}: attn_fwd+attn_bwd+attn_bwd_bwd, B={B} H={H} L={L} D={D}, non-causal",
+            "B": B,
+            "H": H,
+            "L": L,
+            "D": D,
+            "parallelism": "single GPU",
+        },
+        "pct_bf16_peak": round(100 * tflops / roofline.PEAK_BF16_TFLOPS, 2),
+        "pct_attainable_roofline": round(100 * t_roof / (ms_step * 1e-3), 1),
+        "phases": phases,
+        "roofline": roof,
+        "parity_max_rel_err": float(f"{err:.3e}"),
+    }
+    if not args.no_cpu and args.cpu_budget > 0:
+        log("timing the CPU oracle baseline")
+        cb = cpu_baseline(cfg, scale, args.cpu_budget)
+        out["cpu_baseline"] = cb
+        out["speedup_vs_cpu"] = round(tflops / cb["value"], 1) if cb["value"] > 0 else None
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
