@@ -245,37 +245,91 @@ template <typename T> __device__ __forceinline__ f32x4 mma_seq(f32x4 acc, const 
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
-// Cooperative staging of one other-side chunk (rows x0 .. x0 + CH - 1) into LDS, natural and/or transposed.
+// Register-staged chunk loads: every thread issues the global loads of its share of N tensors' chunk at once
+// (``load``), keeps them in flight while the previous chunk is computed, then writes them to LDS, natural and/or
+// transposed (``store``). Workgroups have at least MIN_THREADS threads, which fixes the per-thread share.
 // ---------------------------------------------------------------------------------------------------------------------
 
-template <typename T, int DP, bool NAT, bool TR>
-__device__ __forceinline__ void stage_chunk(T* Xn, T* Xt, const T* base, int64_t srow, int x0, int L, int D, int tid,
-                                            int nthr) {
+constexpr int MIN_THREADS = 256;
+
+template <typename T, int N> struct Src {
+    const T* p[N];
+    int64_t srow[N];
+};
+
+template <typename T, int DP, int N> struct Stage {
     using LY = Lay<T, DP>;
-    constexpr int VPR = DP / LY::VEC;  // 16-byte vectors per row
-    for (int it = tid; it < CH * VPR; it += nthr) {
-        const int x = it % CH;           // consecutive lanes take consecutive rows (conflict-free transposed writes)
-        const int c = it / CH;
-        const int row = x0 + x;
-        const int d0 = c * LY::VEC;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (row < L && d0 < D) val = *reinterpret_cast<const u32x4*>(base + (int64_t)row * srow + d0);
-        if constexpr (NAT) *reinterpret_cast<u32x4*>(Xn + x * LY::PN + d0) = val;
-        if constexpr (TR) {
-            const int col = tr_col<T>(x);
-            if constexpr (ET<T>::F32) {
-                const f32x4 e = __builtin_bit_cast(f32x4, val);
+    static constexpr int VPR = DP / LY::VEC;  // 16-byte vectors per row
+    static constexpr int TOTAL = CH * VPR;    // vectors per tensor chunk
+    static constexpr int ITEMS = (TOTAL + MIN_THREADS - 1) / MIN_THREADS;
+    u32x4 r[N][ITEMS];
+
+    __device__ __forceinline__ void load(const Src<T, N>& s, int x0, int L, int D, int tid, int nthr) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) Xt[(d0 + j) * LY::PT + col] = e[j];
-            } else {
-                using V8 = typename ET<T>::v8;
-                const V8 e = __builtin_bit_cast(V8, val);
+        for (int i = 0; i < ITEMS; ++i) {
+            const int it = tid + i * nthr;
+            const int x = it % CH;  // consecutive lanes take consecutive rows (conflict-free transposed writes)
+            const int c = it / CH;
+            const int row = x0 + x;
+            const int d0 = c * LY::VEC;
+            const bool ok = it < TOTAL && row < L && d0 < D;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) Xt[(d0 + j) * LY::PT + col] = e[j];
+            for (int t = 0; t < N; ++t) {
+                u32x4 z = {0u, 0u, 0u, 0u};
+                r[t][i] = ok ? *reinterpret_cast<const u32x4*>(s.p[t] + (int64_t)row * s.srow[t] + d0) : z;
             }
         }
     }
-}
+
+    // Xn[t] / Xt[t] may be null (that layout is not wanted for tensor t).
+    __device__ __forceinline__ void store(T* const (&Xn)[N], T* const (&Xt)[N], int tid, int nthr) const {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+            const int it = tid + i * nthr;
+            if (it >= TOTAL) continue;
+            const int x = it % CH;
+            const int c = it / CH;
+            const int d0 = c * LY::VEC;
+            const int col = tr_col<T>(x);
+#pragma unroll
+            for (int t = 0; t < N; ++t) {
+                if (Xn[t]) *reinterpret_cast<u32x4*>(Xn[t] + x * LY::PN + d0) = r[t][i];
+                if (Xt[t]) {
+                    T* p = Xt[t] + d0 * LY::PT + col;
+                    if constexpr (ET<T>::F32) {
+                        const f32x4 e = __builtin_bit_cast(f32x4, r[t][i]);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) p[j * LY::PT] = e[j];
+                    } else {
+                        using V8 = typename ET<T>::v8;
+                        const V8 e = __builtin_bit_cast(V8, r[t][i]);
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) p[j * LY::PT] = e[j];
+                    }
+                }
+            }
+        }
+    }
+};
+
+// Row statistics of one query chunk for a two-launch col pass: lse (+inf past L) and up to 3 scratch rows.
+template <int NS> struct StatStage {
+    float r[NS + 1];
+    __device__ __forceinline__ void load(const float* lse, const float* stats, int64_t bhl, int64_t row_base, int x0,
+                                         int L, int tid) {
+        const int x = x0 + tid;
+        const bool ok = tid < CH && x < L;
+        r[0] = ok ? lse[row_base + x] : INFINITY;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) r[s + 1] = ok ? stats[s * bhl + row_base + x] : 0.f;
+    }
+    __device__ __forceinline__ void store(float* st, int tid) const {
+        if (tid < CH) {
+#pragma unroll
+            for (int s = 0; s <= NS; ++s) st[s * CH + tid] = r[s];
+        }
+    }
+};
 
 // ---------------------------------------------------------------------------------------------------------------------
 // Row stores of seq-contraction outputs: lane (own, g) of tile t holds d = 16 t + 4 g + r.

@@ -114,12 +114,14 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd(Args 
     const int row0 = blk * 16 * W + w.wave * 16;
     const int own = row0 + w.l16;
     const bool active = row0 < L;
-    const T* Q = slice<T>(a.q, b, h);
-    const T* K = slice<T>(a.k, b, h);
-    const T* V = slice<T>(a.v, b, h);
+    const Src<T, 2> src = {{slice<T>(a.k, b, h), slice<T>(a.v, b, h)}, {a.k.sl, a.v.sl}};
+    T* const nat[2] = {Kn, nullptr};
+    T* const tr[2] = {nullptr, Vt};
+    Stage<T, DP, 2> stg;
+    stg.load(src, 0, L, D, w.tid, w.nthr);
 
     OwnFrag<T, DP> qf;
-    load_own<T, DP>(qf, Q, a.q.sl, own, L, D, w.g);
+    load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, D, w.g);
     float m = -INFINITY, lsum = 0.f;
     f32x4 acc[LY::NT];
 #pragma unroll
@@ -128,9 +130,9 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd(Args 
 
     for (int x0 = 0; x0 < L; x0 += CH) {
         __syncthreads();
-        stage_chunk<T, DP, true, false>(Kn, nullptr, K, a.k.sl, x0, L, D, w.tid, w.nthr);
-        stage_chunk<T, DP, false, true>(nullptr, Vt, V, a.v.sl, x0, L, D, w.tid, w.nthr);
+        stg.store(nat, tr, w.tid, w.nthr);
         __syncthreads();
+        if (x0 + CH < L) stg.load(src, x0 + CH, L, D, w.tid, w.nthr);
         if (!active) continue;
         f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
         mma_d<T, DP>(s0, Kn, qf, w.l16, w.g);
@@ -174,49 +176,65 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd(Args 
 // Backward
 // =====================================================================================================================
 
-// Row pass: own = 16 query rows per wave; dQ = s sum_j dS[i][j] K[j]. Writes Dr (and lse) for the col pass:
-// FUSED -> LDS array st ([lse | Dr], STAT_MAX each, indexed by query row), else -> a.stats (Dr only).
-template <typename T, int DP, bool FUSED>
-__device__ __forceinline__ void bwd_row(const Args& a, int bh, int own_base, unsigned char* smem, float* st) {
-    using LY = Lay<T, DP>;
-    T* Kn = reinterpret_cast<T*>(smem);
-    T* Vn = reinterpret_cast<T*>(smem + LY::NATB);
-    T* Kt = reinterpret_cast<T*>(smem + 2 * LY::NATB);
-    const WaveIds w = wave_ids();
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int L = a.L, D = a.D;
-    const int row0 = own_base + w.wave * 16;
-    const int own = row0 + w.l16;
-    const bool active = row0 < L;
-    const T* K = slice<T>(a.k, b, h);
-    const T* V = slice<T>(a.v, b, h);
-    const float sc = a.scale;
+// LDS layout of one chunk stage: NN natural tiles followed by NTR transposed tiles.
+template <typename T, int DP> __device__ __forceinline__ T* nat_tile(unsigned char* smem, int i) {
+    return reinterpret_cast<T*>(smem + i * Lay<T, DP>::NATB);
+}
+template <typename T, int DP> __device__ __forceinline__ T* tr_tile(unsigned char* smem, int nn, int i) {
+    return reinterpret_cast<T*>(smem + nn * Lay<T, DP>::NATB + i * Lay<T, DP>::TRB);
+}
 
-    OwnFrag<T, DP> qf, df, of;
-    load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, D, w.g);
-    load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, D, w.g);
-    load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * D, D, own, L, D, w.g);
-    const float dr = xsum4(frag_dot<T, DP>(df, of));
-    const float lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
-    if (w.g == 0 && active) {
-        if constexpr (FUSED) {
-            st[own] = (own < L) ? lse : INFINITY;
-            st[STAT_MAX + own] = (own < L) ? dr : 0.f;
-        } else {
-            if (own < L) a.stats[(int64_t)bh * L + own] = dr;
+// Row pass (own = 16 query rows per wave): dQ = s sum_j dS[i][j] K[j]. Other side per chunk: K (natural, transposed),
+// V (natural). Publishes lse and Dr of its rows: FUSED -> LDS st ([lse | Dr], STAT_MAX each), else Dr -> a.stats.
+template <typename T, int DP, bool FUSED> struct BwdRow {
+    using LY = Lay<T, DP>;
+    static constexpr int NN = 2, NTR = 1, SMEM = NN * LY::NATB + NTR * LY::TRB;
+    OwnFrag<T, DP> qf, df;
+    f32x4 acc[LY::NT];
+    float dr, lse;
+    int own, bh;
+    bool active;
+
+    __device__ __forceinline__ Src<T, 2> src(const Args& a, int b, int h) const {
+        return {{slice<T>(a.k, b, h), slice<T>(a.v, b, h)}, {a.k.sl, a.v.sl}};
+    }
+    __device__ __forceinline__ void lds(unsigned char* smem, T* (&nat)[2], T* (&tr)[2]) const {
+        nat[0] = nat_tile<T, DP>(smem, 0);
+        nat[1] = nat_tile<T, DP>(smem, 1);
+        tr[0] = tr_tile<T, DP>(smem, NN, 0);
+        tr[1] = nullptr;
+    }
+    __device__ __forceinline__ void init(const Args& a, int bh_, int own_base, const WaveIds& w, float* st) {
+        bh = bh_;
+        const int b = bh / a.H, h = bh - b * a.H;
+        const int L = a.L, D = a.D;
+        const int row0 = own_base + w.wave * 16;
+        own = row0 + w.l16;
+        active = row0 < L;
+        OwnFrag<T, DP> of;
+        load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, D, w.g);
+        load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, D, w.g);
+        load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * D, D, own, L, D, w.g);
+        lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
+        dr = xsum4(frag_dot<T, DP>(df, of));
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (w.g == 0 && active) {
+            if constexpr (FUSED) {
+                st[own] = (own < L) ? lse : INFINITY;
+                st[STAT_MAX + own] = (own < L) ? dr : 0.f;
+            } else {
+                if (own < L) a.stats[(int64_t)bh * L + own] = dr;
+            }
         }
     }
-
-    f32x4 acc[LY::NT];
-#pragma unroll
-    for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
-        stage_chunk<T, DP, true, true>(Kn, Kt, K, a.k.sl, x0, L, D, w.tid, w.nthr);
-        stage_chunk<T, DP, true, false>(Vn, nullptr, V, a.v.sl, x0, L, D, w.tid, w.nthr);
-        __syncthreads();
-        if (!active) continue;
+    __device__ __forceinline__ void chunk(const Args& a, int x0, unsigned char* smem, const WaveIds& w) {
+        if (!active) return;
+        const T* Kn = nat_tile<T, DP>(smem, 0);
+        const T* Vn = nat_tile<T, DP>(smem, 1);
+        const T* Kt = tr_tile<T, DP>(smem, NN, 0);
+        const int L = a.L;
+        const float sc = a.scale;
         f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
         mma_d<T, DP>(p0, Kn, qf, w.l16, w.g);
         mma_d<T, DP>(p1, Kn + 16 * LY::PN, qf, w.l16, w.g);
@@ -234,56 +252,53 @@ __device__ __forceinline__ void bwd_row(const Args& a, int bh, int own_base, uns
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], read_seqa<T, DP>(Kt, t, w.l16, w.g), dsb);
     }
-    if (active && own < L) store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * D, acc, sc, D, w.g);
-}
+    __device__ __forceinline__ void finish(const Args& a, const WaveIds& w) {
+        if (active && own < a.L) store_rows<T, DP>(a.out0, ((int64_t)bh * a.L + own) * a.D, acc, a.scale, a.D, w.g);
+    }
+};
 
-// Col pass: own = 16 key rows per wave; dK = s sum_i dS[i][j] Q[i], dV = sum_i P[i][j] dO[i].
-// FUSED -> row statistics from the LDS array st (full length); else staged per chunk from a.lse / a.stats.
-template <typename T, int DP, bool FUSED>
-__device__ __forceinline__ void bwd_col(const Args& a, int bh, int own_base, unsigned char* smem, const float* st) {
+// Col pass (own = 16 key rows per wave): dK = s sum_i dS[i][j] Q[i], dV = sum_i P[i][j] dO[i]. Other side per chunk:
+// Q and dO (natural and transposed); row statistics lse, Dr from ``st`` with row stride ``ss``.
+template <typename T, int DP> struct BwdCol {
     using LY = Lay<T, DP>;
-    T* Qn = reinterpret_cast<T*>(smem);
-    T* On = reinterpret_cast<T*>(smem + LY::NATB);  // dO natural
-    T* Qt = reinterpret_cast<T*>(smem + 2 * LY::NATB);
-    T* Ot = reinterpret_cast<T*>(smem + 2 * LY::NATB + LY::TRB);  // dO transposed
-    float* stc = reinterpret_cast<float*>(smem + 2 * LY::NATB + 2 * LY::TRB);
-    const WaveIds w = wave_ids();
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int L = a.L, D = a.D;
-    const int row0 = own_base + w.wave * 16;
-    const int own = row0 + w.l16;
-    const bool active = row0 < L;
-    const T* Q = slice<T>(a.q, b, h);
-    const T* dO = slice<T>(a.dO, b, h);
-    const float sc = a.scale;
-
+    static constexpr int NN = 2, NTR = 2, SMEM = NN * LY::NATB + NTR * LY::TRB;
     OwnFrag<T, DP> kf, vf;
-    load_own<T, DP>(kf, slice<T>(a.k, b, h), a.k.sl, own, L, D, w.g);
-    load_own<T, DP>(vf, slice<T>(a.v, b, h), a.v.sl, own, L, D, w.g);
     f32x4 ak[LY::NT], av[LY::NT];
-#pragma unroll
-    for (int t = 0; t < LY::NT; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int own, bh;
+    bool active;
 
-    for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
-        stage_chunk<T, DP, true, true>(Qn, Qt, Q, a.q.sl, x0, L, D, w.tid, w.nthr);
-        stage_chunk<T, DP, true, true>(On, Ot, dO, a.dO.sl, x0, L, D, w.tid, w.nthr);
-        if constexpr (!FUSED) {
-            for (int i = w.tid; i < CH; i += w.nthr) {
-                const int x = x0 + i;
-                const int64_t r = (int64_t)bh * L + x;
-                stc[i] = (x < L) ? a.lse[r] : INFINITY;
-                stc[CH + i] = (x < L) ? a.stats[r] : 0.f;
-            }
-        }
-        __syncthreads();
-        if (!active) continue;
-        const float* sl = FUSED ? st + x0 : stc;
-        const float* sd = FUSED ? st + STAT_MAX + x0 : stc + CH;
-        const f32x4 l0 = *reinterpret_cast<const f32x4*>(sl + 4 * w.g);
-        const f32x4 l1 = *reinterpret_cast<const f32x4*>(sl + 16 + 4 * w.g);
-        const f32x4 r0 = *reinterpret_cast<const f32x4*>(sd + 4 * w.g);
-        const f32x4 r1 = *reinterpret_cast<const f32x4*>(sd + 16 + 4 * w.g);
+    __device__ __forceinline__ Src<T, 2> src(const Args& a, int b, int h) const {
+        return {{slice<T>(a.q, b, h), slice<T>(a.dO, b, h)}, {a.q.sl, a.dO.sl}};
+    }
+    __device__ __forceinline__ void lds(unsigned char* smem, T* (&nat)[2], T* (&tr)[2]) const {
+        nat[0] = nat_tile<T, DP>(smem, 0);
+        nat[1] = nat_tile<T, DP>(smem, 1);
+        tr[0] = tr_tile<T, DP>(smem, NN, 0);
+        tr[1] = tr_tile<T, DP>(smem, NN, 1);
+    }
+    __device__ __forceinline__ void init(const Args& a, int bh_, int own_base, const WaveIds& w) {
+        bh = bh_;
+        const int b = bh / a.H, h = bh - b * a.H;
+        const int row0 = own_base + w.wave * 16;
+        own = row0 + w.l16;
+        active = row0 < a.L;
+        load_own<T, DP>(kf, slice<T>(a.k, b, h), a.k.sl, own, a.L, a.D, w.g);
+        load_own<T, DP>(vf, slice<T>(a.v, b, h), a.v.sl, own, a.L, a.D, w.g);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    __device__ __forceinline__ void chunk(const Args& a, unsigned char* smem, const float* st, int ss,
+                                          const WaveIds& w) {
+        if (!active) return;
+        const T* Qn = nat_tile<T, DP>(smem, 0);
+        const T* On = nat_tile<T, DP>(smem, 1);
+        const T* Qt = tr_tile<T, DP>(smem, NN, 0);
+        const T* Ot = tr_tile<T, DP>(smem, NN, 1);
+        const float sc = a.scale;
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(st + 4 * w.g);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(st + 16 + 4 * w.g);
+        const f32x4 r0 = *reinterpret_cast<const f32x4*>(st + ss + 4 * w.g);
+        const f32x4 r1 = *reinterpret_cast<const f32x4*>(st + ss + 16 + 4 * w.g);
         f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
         mma_d<T, DP>(p0, Qn, kf, w.l16, w.g);
         mma_d<T, DP>(p1, Qn + 16 * LY::PN, kf, w.l16, w.g);
@@ -304,109 +319,83 @@ __device__ __forceinline__ void bwd_col(const Args& a, int bh, int own_base, uns
             ak[t] = mma_seq<T>(ak[t], read_seqa<T, DP>(Qt, t, w.l16, w.g), dsb);
         }
     }
-    if (active && own < L) {
-        const int64_t r = ((int64_t)bh * L + own) * D;
-        store_rows<T, DP>(a.out1, r, ak, sc, D, w.g);
-        store_rows<T, DP>(a.out2, r, av, 1.f, D, w.g);
+    __device__ __forceinline__ void finish(const Args& a, const WaveIds& w) {
+        if (active && own < a.L) {
+            const int64_t r = ((int64_t)bh * a.L + own) * a.D;
+            store_rows<T, DP>(a.out1, r, ak, a.scale, a.D, w.g);
+            store_rows<T, DP>(a.out2, r, av, 1.f, a.D, w.g);
+        }
     }
-}
-
-template <typename T, int DP> struct BwdSmem {
-    using LY = Lay<T, DP>;
-    static constexpr int ROW = 2 * LY::NATB + LY::TRB;
-    static constexpr int COL = 2 * LY::NATB + 2 * LY::TRB + 2 * CH * 4;
-    static constexpr int PASS = ROW > COL ? ROW : COL;
 };
-
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_fused(Args a) {
-    __shared__ __align__(16) unsigned char smem[BwdSmem<T, DP>::PASS];
-    __shared__ __align__(16) float st[2 * STAT_MAX];
-    for (int i = threadIdx.x; i < STAT_MAX; i += blockDim.x) {
-        st[i] = INFINITY;
-        st[STAT_MAX + i] = 0.f;
-    }
-    __syncthreads();
-    const int bh = blockIdx.x;
-    bwd_row<T, DP, true>(a, bh, 0, smem, st);
-    bwd_col<T, DP, true>(a, bh, 0, smem, st);
-}
-
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_row(Args a) {
-    __shared__ __align__(16) unsigned char smem[BwdSmem<T, DP>::ROW];
-    int bh, blk;
-    decode_block(a, bh, blk);
-    bwd_row<T, DP, false>(a, bh, blk * (int)blockDim.x / 4, smem, nullptr);
-}
-
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_col(Args a) {
-    __shared__ __align__(16) unsigned char smem[BwdSmem<T, DP>::COL];
-    int bh, blk;
-    decode_block(a, bh, blk);
-    bwd_col<T, DP, false>(a, bh, blk * (int)blockDim.x / 4, smem, nullptr);
-}
 
 // =====================================================================================================================
 // Backward of the backward
 // =====================================================================================================================
 
-// Row pass: own = 16 query rows per wave, streaming form (E and T are known only at the end of the row):
+// Row pass (own = 16 query rows per wave), streaming form (E and T are known only at the end of the row):
 //   X = sum_j (dS A + P Bm) K + dS gK,  U = dS K,  Z = P K,  W = (P A) V + P gV,
 //   hQ = s (X - E U - T Z),  hdO = W - E O.
-// Writes lse, Dr, E, T of its rows: FUSED -> LDS st ([lse | Dr | E | T]), else -> a.stats ([Dr | E | T]).
-template <typename T, int DP, bool FUSED>
-__device__ __forceinline__ void bb_row(const Args& a, int bh, int own_base, unsigned char* smem, float* st) {
+// Other side per chunk: K, gK, V, gV (natural and transposed). Publishes lse, Dr, E, T of its rows:
+// FUSED -> LDS st ([lse | Dr | E | T], STAT_MAX each), else Dr, E, T -> a.stats.
+template <typename T, int DP, bool FUSED> struct BbRow {
     using LY = Lay<T, DP>;
-    T* Kn = reinterpret_cast<T*>(smem);
-    T* gKn = reinterpret_cast<T*>(smem + LY::NATB);
-    T* Vn = reinterpret_cast<T*>(smem + 2 * LY::NATB);
-    T* gVn = reinterpret_cast<T*>(smem + 3 * LY::NATB);
-    T* Kt = reinterpret_cast<T*>(smem + 4 * LY::NATB);
-    T* gKt = reinterpret_cast<T*>(smem + 4 * LY::NATB + LY::TRB);
-    T* Vt = reinterpret_cast<T*>(smem + 4 * LY::NATB + 2 * LY::TRB);
-    T* gVt = reinterpret_cast<T*>(smem + 4 * LY::NATB + 3 * LY::TRB);
-    const WaveIds w = wave_ids();
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int L = a.L, D = a.D;
-    const int row0 = own_base + w.wave * 16;
-    const int own = row0 + w.l16;
-    const bool active = row0 < L;
-    const T* K = slice<T>(a.k, b, h);
-    const T* gK = slice<T>(a.gk, b, h);
-    const T* V = slice<T>(a.v, b, h);
-    const T* gV = slice<T>(a.gv, b, h);
-    const T* O = reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * D;
-    const float sc = a.scale;
-
-    OwnFrag<T, DP> qf, gqf, df, of;
-    load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, D, w.g);
-    load_own<T, DP>(gqf, slice<T>(a.gq, b, h), a.gq.sl, own, L, D, w.g);
-    load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, D, w.g);
-    load_own<T, DP>(of, O, D, own, L, D, w.g);
-    const float dr = xsum4(frag_dot<T, DP>(df, of));
-    const float lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
-
+    static constexpr int NN = 4, NTR = 4, SMEM = NN * LY::NATB + NTR * LY::TRB;
+    OwnFrag<T, DP> qf, gqf, df;
     f32x4 X[LY::NT], U[LY::NT], Z[LY::NT], Wv[LY::NT];
-#pragma unroll
-    for (int t = 0; t < LY::NT; ++t) X[t] = U[t] = Z[t] = Wv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float e_acc = 0.f, t_acc = 0.f;
+    float dr, lse, e_acc, t_acc;
+    int own, bh;
+    bool active;
 
-    for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
-        stage_chunk<T, DP, true, true>(Kn, Kt, K, a.k.sl, x0, L, D, w.tid, w.nthr);
-        stage_chunk<T, DP, true, true>(gKn, gKt, gK, a.gk.sl, x0, L, D, w.tid, w.nthr);
-        stage_chunk<T, DP, true, true>(Vn, Vt, V, a.v.sl, x0, L, D, w.tid, w.nthr);
-        stage_chunk<T, DP, true, true>(gVn, gVt, gV, a.gv.sl, x0, L, D, w.tid, w.nthr);
-        __syncthreads();
-        if (!active) continue;
+    __device__ __forceinline__ Src<T, 4> src(const Args& a, int b, int h) const {
+        return {{slice<T>(a.k, b, h), slice<T>(a.gk, b, h), slice<T>(a.v, b, h), slice<T>(a.gv, b, h)},
+                {a.k.sl, a.gk.sl, a.v.sl, a.gv.sl}};
+    }
+    __device__ __forceinline__ void lds(unsigned char* smem, T* (&nat)[4], T* (&tr)[4]) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            nat[i] = nat_tile<T, DP>(smem, i);
+            tr[i] = tr_tile<T, DP>(smem, NN, i);
+        }
+    }
+    __device__ __forceinline__ void init(const Args& a, int bh_, int own_base, const WaveIds& w) {
+        bh = bh_;
+        const int b = bh / a.H, h = bh - b * a.H;
+        const int L = a.L, D = a.D;
+        const int row0 = own_base + w.wave * 16;
+        own = row0 + w.l16;
+        active = row0 < L;
+        OwnFrag<T, DP> of;
+        load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, D, w.g);
+        load_own<T, DP>(gqf, slice<T>(a.gq, b, h), a.gq.sl, own, L, D, w.g);
+        load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, D, w.g);
+        load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * D, D, own, L, D, w.g);
+        lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
+        dr = xsum4(frag_dot<T, DP>(df, of));
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) X[t] = U[t] = Z[t] = Wv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        e_acc = t_acc = 0.f;
+    }
+    __device__ __forceinline__ void chunk(const Args& a, int x0, unsigned char* smem, const WaveIds& w) {
+        if (!active) return;
+        const T* Kn = nat_tile<T, DP>(smem, 0);
+        const T* gKn = nat_tile<T, DP>(smem, 1);
+        const T* Vn = nat_tile<T, DP>(smem, 2);
+        const T* gVn = nat_tile<T, DP>(smem, 3);
+        const T* Kt = tr_tile<T, DP>(smem, NN, 0);
+        const T* gKt = tr_tile<T, DP>(smem, NN, 1);
+        const T* Vt = tr_tile<T, DP>(smem, NN, 2);
+        const T* gVt = tr_tile<T, DP>(smem, NN, 3);
+        const int L = a.L;
+        const float sc = a.scale;
         f32x4 p[2], dp[2], at[2], bm[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
             const int off = hh * 16 * LY::PN;
             mma_d<T, DP>(p[hh], Kn + off, qf, w.l16, w.g);
-            mma_d<T, DP>(dp[hh], Vn + off, df, w.l16, w.g);
             mma_d<T, DP>(at[hh], Kn + off, gqf, w.l16, w.g);
             mma_d<T, DP>(at[hh], gKn + off, qf, w.l16, w.g);
+            mma_d<T, DP>(dp[hh], Vn + off, df, w.l16, w.g);
             mma_d<T, DP>(bm[hh], gVn + off, df, w.l16, w.g);
         }
         f32x4 ds[2], pa[2], m1[2];
@@ -441,113 +430,108 @@ __device__ __forceinline__ void bb_row(const Args& a, int bh, int own_base, unsi
             Wv[t] = mma_seq<T>(Wv[t], read_seqa<T, DP>(gVt, t, w.l16, w.g), pb);
         }
     }
-    const float E = xsum4(e_acc);
-    const float Tm = xsum4(t_acc);
-    if (active && own < L) {
-        const int64_t r = ((int64_t)bh * L + own) * D;
+    __device__ __forceinline__ void finish(const Args& a, const WaveIds& w, float* st) {
+        const float E = xsum4(e_acc);
+        const float Tm = xsum4(t_acc);
+        const int L = a.L, D = a.D;
+        if (active && own < L) {
+            const int64_t r = ((int64_t)bh * L + own) * D;
+            const T* O = reinterpret_cast<const T*>(a.o) + r;
 #pragma unroll
-        for (int t = 0; t < LY::NT; ++t) {
-            const int d = 16 * t + 4 * w.g;
-            if (d < D) {
-                const f32x4 hq = (X[t] - E * U[t] - Tm * Z[t]) * sc;
-                const f32x4 hdo = Wv[t] - E * load4<T>(O + (int64_t)own * D + d);
-                store4<T>(reinterpret_cast<T*>(a.out0) + r + d, hq);
-                store4<T>(reinterpret_cast<T*>(a.out3) + r + d, hdo);
+            for (int t = 0; t < LY::NT; ++t) {
+                const int d = 16 * t + 4 * w.g;
+                if (d < D) {
+                    const f32x4 hq = (X[t] - E * U[t] - Tm * Z[t]) * a.scale;
+                    const f32x4 hdo = Wv[t] - E * load4<T>(O + d);
+                    store4<T>(reinterpret_cast<T*>(a.out0) + r + d, hq);
+                    store4<T>(reinterpret_cast<T*>(a.out3) + r + d, hdo);
+                }
+            }
+        }
+        if (w.g == 0 && active) {
+            if constexpr (FUSED) {
+                const bool ok = own < L;
+                st[own] = ok ? lse : INFINITY;
+                st[STAT_MAX + own] = ok ? dr : 0.f;
+                st[2 * STAT_MAX + own] = ok ? E : 0.f;
+                st[3 * STAT_MAX + own] = ok ? Tm : 0.f;
+            } else if (own < L) {
+                const int64_t r = (int64_t)bh * L + own;
+                a.stats[r] = dr;
+                a.stats[a.bhl + r] = E;
+                a.stats[2 * a.bhl + r] = Tm;
             }
         }
     }
-    if (w.g == 0 && active) {
-        if constexpr (FUSED) {
-            const bool ok = own < L;
-            st[own] = ok ? lse : INFINITY;
-            st[STAT_MAX + own] = ok ? dr : 0.f;
-            st[2 * STAT_MAX + own] = ok ? E : 0.f;
-            st[3 * STAT_MAX + own] = ok ? Tm : 0.f;
-        } else if (own < L) {
-            const int64_t r = (int64_t)bh * L + own;
-            a.stats[r] = dr;
-            a.stats[a.bhl + r] = E;
-            a.stats[2 * a.bhl + r] = Tm;
-        }
-    }
-}
+};
 
-// Col pass: own = 16 key rows per wave; hK = s sum_i (dS2[i][j] Q[i] + dS[i][j] gQ[i]), hV = sum_i Pa[i][j] dO[i].
-template <typename T, int DP, bool FUSED>
-__device__ __forceinline__ void bb_col(const Args& a, int bh, int own_base, unsigned char* smem, const float* st) {
+// Col pass (own = 16 key rows per wave): hK = s sum_i (dS2[i][j] Q[i] + dS[i][j] gQ[i]), hV = sum_i Pa[i][j] dO[i].
+// Other side per chunk: Q, gQ, dO (natural and transposed); row statistics lse, Dr, E, T from ``st`` (stride ``ss``).
+template <typename T, int DP> struct BbCol {
     using LY = Lay<T, DP>;
-    T* Qn = reinterpret_cast<T*>(smem);
-    T* gQn = reinterpret_cast<T*>(smem + LY::NATB);
-    T* On = reinterpret_cast<T*>(smem + 2 * LY::NATB);  // dO natural
-    T* Qt = reinterpret_cast<T*>(smem + 3 * LY::NATB);
-    T* gQt = reinterpret_cast<T*>(smem + 3 * LY::NATB + LY::TRB);
-    T* Ot = reinterpret_cast<T*>(smem + 3 * LY::NATB + 2 * LY::TRB);  // dO transposed
-    float* stc = reinterpret_cast<float*>(smem + 3 * LY::NATB + 3 * LY::TRB);
-    const WaveIds w = wave_ids();
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int L = a.L, D = a.D;
-    const int row0 = own_base + w.wave * 16;
-    const int own = row0 + w.l16;
-    const bool active = row0 < L;
-    const T* Q = slice<T>(a.q, b, h);
-    const T* gQ = slice<T>(a.gq, b, h);
-    const T* dO = slice<T>(a.dO, b, h);
-    const float sc = a.scale;
-
+    static constexpr int NN = 3, NTR = 3, SMEM = NN * LY::NATB + NTR * LY::TRB;
     OwnFrag<T, DP> kf, gkf, vf, gvf;
-    load_own<T, DP>(kf, slice<T>(a.k, b, h), a.k.sl, own, L, D, w.g);
-    load_own<T, DP>(gkf, slice<T>(a.gk, b, h), a.gk.sl, own, L, D, w.g);
-    load_own<T, DP>(vf, slice<T>(a.v, b, h), a.v.sl, own, L, D, w.g);
-    load_own<T, DP>(gvf, slice<T>(a.gv, b, h), a.gv.sl, own, L, D, w.g);
     f32x4 hk[LY::NT], hv[LY::NT];
-#pragma unroll
-    for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int own, bh;
+    bool active;
 
-    for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
-        stage_chunk<T, DP, true, true>(Qn, Qt, Q, a.q.sl, x0, L, D, w.tid, w.nthr);
-        stage_chunk<T, DP, true, true>(gQn, gQt, gQ, a.gq.sl, x0, L, D, w.tid, w.nthr);
-        stage_chunk<T, DP, true, true>(On, Ot, dO, a.dO.sl, x0, L, D, w.tid, w.nthr);
-        if constexpr (!FUSED) {
-            for (int i = w.tid; i < CH; i += w.nthr) {
-                const int x = x0 + i;
-                const int64_t r = (int64_t)bh * L + x;
-                const bool ok = x < L;
-                stc[i] = ok ? a.lse[r] : INFINITY;
-                stc[CH + i] = ok ? a.stats[r] : 0.f;
-                stc[2 * CH + i] = ok ? a.stats[a.bhl + r] : 0.f;
-                stc[3 * CH + i] = ok ? a.stats[2 * a.bhl + r] : 0.f;
-            }
+    __device__ __forceinline__ Src<T, 3> src(const Args& a, int b, int h) const {
+        return {{slice<T>(a.q, b, h), slice<T>(a.gq, b, h), slice<T>(a.dO, b, h)}, {a.q.sl, a.gq.sl, a.dO.sl}};
+    }
+    __device__ __forceinline__ void lds(unsigned char* smem, T* (&nat)[3], T* (&tr)[3]) const {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            nat[i] = nat_tile<T, DP>(smem, i);
+            tr[i] = tr_tile<T, DP>(smem, NN, i);
         }
-        __syncthreads();
-        if (!active) continue;
-        const int sstride = FUSED ? STAT_MAX : CH;
-        const float* s_base = FUSED ? st + x0 : stc;
+    }
+    __device__ __forceinline__ void init(const Args& a, int bh_, int own_base, const WaveIds& w) {
+        bh = bh_;
+        const int b = bh / a.H, h = bh - b * a.H;
+        const int row0 = own_base + w.wave * 16;
+        own = row0 + w.l16;
+        active = row0 < a.L;
+        load_own<T, DP>(kf, slice<T>(a.k, b, h), a.k.sl, own, a.L, a.D, w.g);
+        load_own<T, DP>(gkf, slice<T>(a.gk, b, h), a.gk.sl, own, a.L, a.D, w.g);
+        load_own<T, DP>(vf, slice<T>(a.v, b, h), a.v.sl, own, a.L, a.D, w.g);
+        load_own<T, DP>(gvf, slice<T>(a.gv, b, h), a.gv.sl, own, a.L, a.D, w.g);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    __device__ __forceinline__ void chunk(const Args& a, unsigned char* smem, const float* st, int ss,
+                                          const WaveIds& w) {
+        if (!active) return;
+        const T* Qn = nat_tile<T, DP>(smem, 0);
+        const T* gQn = nat_tile<T, DP>(smem, 1);
+        const T* On = nat_tile<T, DP>(smem, 2);
+        const T* Qt = tr_tile<T, DP>(smem, NN, 0);
+        const T* gQt = tr_tile<T, DP>(smem, NN, 1);
+        const T* Ot = tr_tile<T, DP>(smem, NN, 2);
+        const float sc = a.scale;
         f32x4 p[2], dp[2], at[2], bm[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
             const int off = hh * 16 * LY::PN;
             mma_d<T, DP>(p[hh], Qn + off, kf, w.l16, w.g);
-            mma_d<T, DP>(dp[hh], On + off, vf, w.l16, w.g);
-            mma_d<T, DP>(at[hh], gQn + off, kf, w.l16, w.g);
             mma_d<T, DP>(at[hh], Qn + off, gkf, w.l16, w.g);
+            mma_d<T, DP>(at[hh], gQn + off, kf, w.l16, w.g);
+            mma_d<T, DP>(dp[hh], On + off, vf, w.l16, w.g);
             mma_d<T, DP>(bm[hh], On + off, gvf, w.l16, w.g);
         }
         f32x4 ds[2], ds2[2], pa[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int so = 16 * hh + 4 * w.g;
-            const f32x4 ls = *reinterpret_cast<const f32x4*>(s_base + so);
-            const f32x4 rs = *reinterpret_cast<const f32x4*>(s_base + sstride + so);
-            const f32x4 es = *reinterpret_cast<const f32x4*>(s_base + 2 * sstride + so);
-            const f32x4 ts = *reinterpret_cast<const f32x4*>(s_base + 3 * sstride + so);
+            const f32x4 ls = *reinterpret_cast<const f32x4*>(st + so);
+            const f32x4 rs = *reinterpret_cast<const f32x4*>(st + ss + so);
+            const f32x4 es = *reinterpret_cast<const f32x4*>(st + 2 * ss + so);
+            const f32x4 ts = *reinterpret_cast<const f32x4*>(st + 3 * ss + so);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float pv = fast_exp2(fmaf(p[hh][r], sc, -ls[r]) * LOG2E);
                 const float dsv = pv * (dp[hh][r] - rs[r]);
                 const float av = at[hh][r] * sc;
-                p[hh][r] = pv;
                 ds[hh][r] = dsv;
                 const float m1 = fmaf(dsv, av, pv * bm[hh][r]);
                 ds2[hh][r] = m1 - es[r] * dsv - ts[r] * pv;
@@ -564,47 +548,186 @@ __device__ __forceinline__ void bb_col(const Args& a, int bh, int own_base, unsi
             hv[t] = mma_seq<T>(hv[t], read_seqa<T, DP>(Ot, t, w.l16, w.g), pab);
         }
     }
-    if (active && own < L) {
-        const int64_t r = ((int64_t)bh * L + own) * D;
-        store_rows<T, DP>(a.out1, r, hk, sc, D, w.g);
-        store_rows<T, DP>(a.out2, r, hv, 1.f, D, w.g);
+    __device__ __forceinline__ void finish(const Args& a, const WaveIds& w) {
+        if (active && own < a.L) {
+            const int64_t r = ((int64_t)bh * a.L + own) * a.D;
+            store_rows<T, DP>(a.out1, r, hk, a.scale, a.D, w.g);
+            store_rows<T, DP>(a.out2, r, hv, 1.f, a.D, w.g);
+        }
     }
-}
-
-template <typename T, int DP> struct BbSmem {
-    using LY = Lay<T, DP>;
-    static constexpr int ROW = 4 * LY::NATB + 4 * LY::TRB;
-    static constexpr int COL = 3 * LY::NATB + 3 * LY::TRB + 4 * CH * 4;
-    static constexpr int PASS = ROW > COL ? ROW : COL;
 };
 
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_fused(Args a) {
-    __shared__ __align__(16) unsigned char smem[BbSmem<T, DP>::PASS];
-    __shared__ __align__(16) float st[4 * STAT_MAX];
-    for (int i = threadIdx.x; i < STAT_MAX; i += blockDim.x) {
-        st[i] = INFINITY;
-        st[STAT_MAX + i] = 0.f;
-        st[2 * STAT_MAX + i] = 0.f;
-        st[3 * STAT_MAX + i] = 0.f;
-    }
-    __syncthreads();
+// =====================================================================================================================
+// Pass drivers. Each chunk: barrier, write the staged registers to LDS, barrier, issue the next chunk's loads (they
+// stay in flight during this chunk's MFMA work), compute. The one-workgroup kernels prefetch the col pass's first
+// chunk during the row pass's last chunk.
+// =====================================================================================================================
+
+template <int NS> struct NoStats {};
+
+template <typename T, int DP, class Row, class Col, int NCOL, int NSTAT>
+__device__ __forceinline__ void fused_two_pass(const Args& a, unsigned char* smem, float* st) {
+    const WaveIds w = wave_ids();
     const int bh = blockIdx.x;
-    bb_row<T, DP, true>(a, bh, 0, smem, st);
-    bb_col<T, DP, true>(a, bh, 0, smem, st);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L, D = a.D;
+    for (int i = w.tid; i < STAT_MAX; i += w.nthr) {
+        st[i] = INFINITY;
+#pragma unroll
+        for (int s = 1; s <= NSTAT; ++s) st[s * STAT_MAX + i] = 0.f;
+    }
+    Row row;
+    const auto rsrc = row.src(a, b, h);
+    constexpr int NROW = sizeof(rsrc.p) / sizeof(rsrc.p[0]);
+    T* rn[NROW];
+    T* rt[NROW];
+    row.lds(smem, rn, rt);
+    Stage<T, DP, NROW> rst;
+    Stage<T, DP, NCOL> cst;
+    Col col;
+    const auto csrc = col.src(a, b, h);
+    T* cn[NCOL];
+    T* ct[NCOL];
+    col.lds(smem, cn, ct);
+
+    rst.load(rsrc, 0, L, D, w.tid, w.nthr);
+    __syncthreads();  // statistics defaults visible before the row pass publishes
+    if constexpr (NSTAT == 1) {
+        row.init(a, bh, 0, w, st);
+    } else {
+        row.init(a, bh, 0, w);
+    }
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        rst.store(rn, rt, w.tid, w.nthr);
+        __syncthreads();
+        if (x0 + CH < L)
+            rst.load(rsrc, x0 + CH, L, D, w.tid, w.nthr);
+        else
+            cst.load(csrc, 0, L, D, w.tid, w.nthr);
+        row.chunk(a, x0, smem, w);
+    }
+    if constexpr (NSTAT == 1) {
+        row.finish(a, w);
+    } else {
+        row.finish(a, w, st);
+    }
+    col.init(a, bh, 0, w);
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        cst.store(cn, ct, w.tid, w.nthr);
+        __syncthreads();
+        if (x0 + CH < L) cst.load(csrc, x0 + CH, L, D, w.tid, w.nthr);
+        col.chunk(a, smem, st + x0, STAT_MAX, w);
+    }
+    col.finish(a, w);
 }
 
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_row(Args a) {
-    __shared__ __align__(16) unsigned char smem[BbSmem<T, DP>::ROW];
-    int bh, blk;
-    decode_block(a, bh, blk);
-    bb_row<T, DP, false>(a, bh, blk * (int)blockDim.x / 4, smem, nullptr);
+template <typename T, int DP> struct FusedSmem {
+    static constexpr int BWD = BwdRow<T, DP, true>::SMEM > BwdCol<T, DP>::SMEM ? BwdRow<T, DP, true>::SMEM
+                                                                                  : BwdCol<T, DP>::SMEM;
+    static constexpr int BB = BbRow<T, DP, true>::SMEM > BbCol<T, DP>::SMEM ? BbRow<T, DP, true>::SMEM
+                                                                             : BbCol<T, DP>::SMEM;
+};
+
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_fused(Args a) {
+    __shared__ __align__(16) unsigned char smem[FusedSmem<T, DP>::BWD];
+    __shared__ __align__(16) float st[2 * STAT_MAX];
+    fused_two_pass<T, DP, BwdRow<T, DP, true>, BwdCol<T, DP>, 2, 1>(a, smem, st);
 }
 
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_col(Args a) {
-    __shared__ __align__(16) unsigned char smem[BbSmem<T, DP>::COL];
+template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_fused(Args a) {
+    __shared__ __align__(16) unsigned char smem[FusedSmem<T, DP>::BB];
+    __shared__ __align__(16) float st[4 * STAT_MAX];
+    fused_two_pass<T, DP, BbRow<T, DP, true>, BbCol<T, DP>, 3, 3>(a, smem, st);
+}
+
+// Two-launch row kernel: own rows [blk * 16 W, (blk + 1) * 16 W) of one (b, h); statistics go to a.stats.
+template <typename T, int DP, class Row, int NROW, bool BB>
+__device__ __forceinline__ void stream_row(const Args& a, unsigned char* smem) {
+    const WaveIds w = wave_ids();
     int bh, blk;
     decode_block(a, bh, blk);
-    bb_col<T, DP, false>(a, bh, blk * (int)blockDim.x / 4, smem, nullptr);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L, D = a.D;
+    Row row;
+    const auto src = row.src(a, b, h);
+    T* rn[NROW];
+    T* rt[NROW];
+    row.lds(smem, rn, rt);
+    Stage<T, DP, NROW> rst;
+    rst.load(src, 0, L, D, w.tid, w.nthr);
+    if constexpr (BB) {
+        row.init(a, bh, blk * (w.nthr >> 2), w);
+    } else {
+        row.init(a, bh, blk * (w.nthr >> 2), w, nullptr);
+    }
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        rst.store(rn, rt, w.tid, w.nthr);
+        __syncthreads();
+        if (x0 + CH < L) rst.load(src, x0 + CH, L, D, w.tid, w.nthr);
+        row.chunk(a, x0, smem, w);
+    }
+    if constexpr (BB) {
+        row.finish(a, w, nullptr);
+    } else {
+        row.finish(a, w);
+    }
+}
+
+// Two-launch col kernel: own rows [blk * 16 W, (blk + 1) * 16 W) of one (b, h); statistics staged from a.lse/a.stats.
+template <typename T, int DP, class Col, int NCOL, int NSTAT>
+__device__ __forceinline__ void stream_col(const Args& a, unsigned char* smem) {
+    const WaveIds w = wave_ids();
+    int bh, blk;
+    decode_block(a, bh, blk);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L, D = a.D;
+    Col col;
+    const auto src = col.src(a, b, h);
+    T* cn[NCOL];
+    T* ct[NCOL];
+    col.lds(smem, cn, ct);
+    float* stc = reinterpret_cast<float*>(smem + Col::SMEM);
+    Stage<T, DP, NCOL> cst;
+    StatStage<NSTAT> sst;
+    const int64_t rb = (int64_t)bh * L;
+    cst.load(src, 0, L, D, w.tid, w.nthr);
+    sst.load(a.lse, a.stats, a.bhl, rb, 0, L, w.tid);
+    col.init(a, bh, blk * (w.nthr >> 2), w);
+    for (int x0 = 0; x0 < L; x0 += CH) {
+        __syncthreads();
+        cst.store(cn, ct, w.tid, w.nthr);
+        sst.store(stc, w.tid);
+        __syncthreads();
+        if (x0 + CH < L) {
+            cst.load(src, x0 + CH, L, D, w.tid, w.nthr);
+            sst.load(a.lse, a.stats, a.bhl, rb, x0 + CH, L, w.tid);
+        }
+        col.chunk(a, smem, stc, CH, w);
+    }
+    col.finish(a, w);
+}
+
+template <typename T, int DP> __global__ __launch_bounds__(256) void k_bwd_row(Args a) {
+    __shared__ __align__(16) unsigned char smem[BwdRow<T, DP, false>::SMEM];
+    stream_row<T, DP, BwdRow<T, DP, false>, 2, false>(a, smem);
+}
+
+template <typename T, int DP> __global__ __launch_bounds__(256) void k_bwd_col(Args a) {
+    __shared__ __align__(16) unsigned char smem[BwdCol<T, DP>::SMEM + 2 * CH * 4];
+    stream_col<T, DP, BwdCol<T, DP>, 2, 1>(a, smem);
+}
+
+template <typename T, int DP> __global__ __launch_bounds__(256) void k_bb_row(Args a) {
+    __shared__ __align__(16) unsigned char smem[BbRow<T, DP, false>::SMEM];
+    stream_row<T, DP, BbRow<T, DP, false>, 4, true>(a, smem);
+}
+
+template <typename T, int DP> __global__ __launch_bounds__(256) void k_bb_col(Args a) {
+    __shared__ __align__(16) unsigned char smem[BbCol<T, DP>::SMEM + 4 * CH * 4];
+    stream_col<T, DP, BbCol<T, DP>, 3, 3>(a, smem);
 }
 
 // =====================================================================================================================
@@ -614,6 +737,12 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_col(Ar
 constexpr int STREAM_WAVES = 4;  // waves (x16 own rows) per workgroup of the two-launch kernels
 
 static bool fused_shape(int L) { return L <= STAT_MAX; }
+
+// One wave per 16 rows, at least MIN_THREADS threads (the chunk staging assumes it).
+static int fused_threads(int L) {
+    const int t = 64 * ((L + 15) / 16);
+    return t < MIN_THREADS ? MIN_THREADS : t;
+}
 
 static int elem_size(int dtype) { return dtype == EBR_DTYPE_F32 ? 4 : 2; }
 
@@ -687,7 +816,7 @@ template <typename T, int DP> struct FwdLaunch {
             a.nblk = 1;
             a.xcd_remap = 0;
             grid = (int)bh;
-            threads = 64 * ((a.L + 15) / 16);
+            threads = fused_threads(a.L);
         } else {
             plan_stream(a, bh, grid, threads);
         }
@@ -702,7 +831,7 @@ template <typename T, int DP> struct BwdLaunch {
         if (fused_shape(a.L)) {
             a.nblk = 1;
             a.xcd_remap = 0;
-            hipLaunchKernelGGL((k_bwd_fused<T, DP>), dim3((int)bh), dim3(64 * ((a.L + 15) / 16)), 0, s, a);
+            hipLaunchKernelGGL((k_bwd_fused<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
             return launch_rc();
         }
         int grid, threads;
@@ -721,7 +850,7 @@ template <typename T, int DP> struct BbLaunch {
         if (fused_shape(a.L)) {
             a.nblk = 1;
             a.xcd_remap = 0;
-            hipLaunchKernelGGL((k_bb_fused<T, DP>), dim3((int)bh), dim3(64 * ((a.L + 15) / 16)), 0, s, a);
+            hipLaunchKernelGGL((k_bb_fused<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
             return launch_rc();
         }
         int grid, threads;
