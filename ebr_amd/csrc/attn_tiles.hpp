@@ -211,6 +211,24 @@ template <typename T> __device__ __forceinline__ SeqB<T> make_seqb(f32x4 p0, f32
     return b;
 }
 
+// The 8 values of a 16-bit SeqB as fp32 (slot order s = 4 h + r) and back.
+template <typename T> __device__ __forceinline__ void unpack_seqb(const SeqB<T>& b, float (&f)[8]) {
+    using V8 = typename ET<T>::v8;
+    const V8 v = __builtin_bit_cast(V8, b.v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (float)v[e];
+}
+
+template <typename T> __device__ __forceinline__ SeqB<T> pack_seqb(const float (&f)[8]) {
+    using V8 = typename ET<T>::v8;
+    V8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (T)f[e];
+    SeqB<T> b;
+    b.v = __builtin_bit_cast(u32x4, v);
+    return b;
+}
+
 template <typename T> struct SeqA {
     u32x4 v;
 };

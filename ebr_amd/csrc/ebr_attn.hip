@@ -24,6 +24,7 @@
 #include <stdint.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "../../include/ebr_attn.h"
 #include "attn_tiles.hpp"
@@ -642,6 +643,8 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_fused(
     fused_two_pass<T, DP, BbRow<T, DP, true>, BbCol<T, DP>, 3, 3>(a, smem, st);
 }
 
+#include "attn_resident.hpp"
+
 // Two-launch row kernel: own rows [blk * 16 W, (blk + 1) * 16 W) of one (b, h); statistics go to a.stats.
 template <typename T, int DP, class Row, int NROW, bool BB>
 __device__ __forceinline__ void stream_row(const Args& a, unsigned char* smem) {
@@ -746,6 +749,21 @@ static int fused_threads(int L) {
 
 static int elem_size(int dtype) { return dtype == EBR_DTYPE_F32 ? 4 : 2; }
 
+// The resident one-workgroup kernels (16-bit inputs): D must be a full chunk width and every slice's byte range
+// (rows 0 .. L-1 of each strided input) must be addressable with 32-bit buffer offsets.
+static bool strided_fits(const Strided& t, int L, int D, int es) {
+    return ((int64_t)(L - 1) * t.sl + D) * es < ((int64_t)1 << 31);
+}
+static bool resident_shape(const Args& a, int dp, int es, bool grads) {
+    if (es != 2 || a.D != dp || a.L > STAT_MAX) return false;
+    bool ok = strided_fits(a.q, a.L, a.D, es) && strided_fits(a.k, a.L, a.D, es) && strided_fits(a.v, a.L, a.D, es);
+    if (grads) {
+        ok = ok && strided_fits(a.dO, a.L, a.D, es) && strided_fits(a.gq, a.L, a.D, es) &&
+             strided_fits(a.gk, a.L, a.D, es) && strided_fits(a.gv, a.L, a.D, es);
+    }
+    return ok;
+}
+
 static int check_shape(int dtype, int B, int H, int L, int D) {
     if (dtype != EBR_DTYPE_F32 && dtype != EBR_DTYPE_BF16 && dtype != EBR_DTYPE_F16) return EBR_ERR_DTYPE;
     if (B < 1 || H < 1 || L < 1 || D < 1 || D > 128) return EBR_ERR_SHAPE;
@@ -811,6 +829,13 @@ static void plan_stream(Args& a, int64_t bh, int& grid, int& threads) {
 template <typename T, int DP> struct FwdLaunch {
     static int run(Args a, hipStream_t s) {
         const int64_t bh = (int64_t)a.B * a.H;
+        if constexpr (!ET<T>::F32) {
+            if (resident_shape(a, DP, 2, false)) {
+                a.nblk = 1;
+                hipLaunchKernelGGL((k_fwd_res<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
+                return launch_rc();
+            }
+        }
         int grid, threads;
         if (fused_shape(a.L)) {
             a.nblk = 1;
@@ -828,6 +853,14 @@ template <typename T, int DP> struct FwdLaunch {
 template <typename T, int DP> struct BwdLaunch {
     static int run(Args a, hipStream_t s) {
         const int64_t bh = (int64_t)a.B * a.H;
+        if constexpr (!ET<T>::F32) {
+            a.gq = a.gk = a.gv = a.dO;  // only q, k, v, dO are read
+            if (resident_shape(a, DP, 2, true)) {
+                a.nblk = 1;
+                hipLaunchKernelGGL((k_bwd_res<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
+                return launch_rc();
+            }
+        }
         if (fused_shape(a.L)) {
             a.nblk = 1;
             a.xcd_remap = 0;
@@ -850,7 +883,17 @@ template <typename T, int DP> struct BbLaunch {
         if (fused_shape(a.L)) {
             a.nblk = 1;
             a.xcd_remap = 0;
-            hipLaunchKernelGGL((k_bb_fused<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
+            const dim3 grid((int)bh), block(fused_threads(a.L));
+            if (!resident_shape(a, DP, (int)sizeof(T), true)) {
+                hipLaunchKernelGGL((k_bb_fused<T, DP>), grid, block, 0, s, a);
+            } else if constexpr (!ET<T>::F32) {
+                switch ((a.L + CH - 1) / CH) {
+                    case 1: hipLaunchKernelGGL((k_bb_res<T, DP, 1>), grid, block, 0, s, a); break;
+                    case 2: hipLaunchKernelGGL((k_bb_res<T, DP, 2>), grid, block, 0, s, a); break;
+                    case 3: hipLaunchKernelGGL((k_bb_res<T, DP, 3>), grid, block, 0, s, a); break;
+                    default: hipLaunchKernelGGL((k_bb_res<T, DP, 4>), grid, block, 0, s, a); break;
+                }
+            }
             return launch_rc();
         }
         int grid, threads;
