@@ -21,16 +21,33 @@ template <int DP> struct Sw {
     static constexpr int NCK = DP / 8;   // 16-byte chunks per row
     static constexpr int ROWB = DP * 2;  // bytes per row
     static constexpr int RPI = 64 / NCK; // rows moved by one 64-lane x 16-byte load
+    // Depends on x mod 16 only, so every 16-row tile (and every 32-row chunk) has the same per-lane pattern.
     static __device__ __forceinline__ int swz(int x) {
         if constexpr (DP == 32) {
             return (x >> 2) & 3;
         } else if constexpr (DP == 64) {
-            return (x ^ (x >> 3)) & 7;
+            return (x & 7) ^ ((x >> 3) & 1);
         } else {
             return x & 15;
         }
     }
     static __device__ __forceinline__ int off(int x, int c) { return x * ROWB + 16 * (c ^ swz(x)); }
+};
+
+// Per-lane byte offsets inside a 16-row tile (a) and a 32-row chunk (tr), fixed for the whole kernel.
+template <typename T, int DP> struct LaneOff {
+    int a[Lay<T, DP>::NC];   // A-operand / own-row read of chunk 4 c + g in row l16
+    int tr[Lay<T, DP>::NT];  // transpose read of d tile t: row 4 g + (l16 >> 2), columns 16 t + 4 (l16 & 3)
+    __device__ __forceinline__ LaneOff(int l16, int g) {
+#pragma unroll
+        for (int c = 0; c < Lay<T, DP>::NC; ++c) a[c] = Sw<DP>::off(l16, 4 * c + g);
+        const int k = l16 >> 2, j = l16 & 3;
+#pragma unroll
+        for (int t = 0; t < Lay<T, DP>::NT; ++t) {
+            const int d = 16 * t + 4 * j;
+            tr[t] = Sw<DP>::off(4 * g + k, d >> 3) + (d & 7) * 2;
+        }
+    }
 };
 
 // Issue the loads of rows [0, Lp) of one (b, h) slice into ``region`` (Lp * ROWB bytes); waves split the 1 KB blocks.
@@ -53,37 +70,34 @@ __device__ __forceinline__ void async_rows(unsigned char* region, const T* slice
 
 __device__ __forceinline__ void async_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
-// Own-side B fragment from a swizzled region (row = own index).
+// Own-side B fragment from a swizzled region: the 16 rows starting at ``row0`` (a multiple of 16), lane row l16.
 template <typename T, int DP>
-__device__ __forceinline__ void own_from_lds(OwnFrag<T, DP>& f, const unsigned char* region, int row, int g) {
+__device__ __forceinline__ void own_from_lds(OwnFrag<T, DP>& f, const unsigned char* region, int row0,
+                                             const LaneOff<T, DP>& lo) {
+    const unsigned char* base = region + row0 * Sw<DP>::ROWB;
 #pragma unroll
-    for (int c = 0; c < Lay<T, DP>::NC; ++c)
-        f.v[c] = *reinterpret_cast<const u32x4*>(region + Sw<DP>::off(row, 4 * c + g));
+    for (int c = 0; c < Lay<T, DP>::NC; ++c) f.v[c] = *reinterpret_cast<const u32x4*>(base + lo.a[c]);
 }
 
-// acc[m = x][n = own] += sum_d X[x][d] Own[own][d] for the 16 rows starting at ``row0`` of a swizzled region.
+// acc[m = x][n = own] += sum_d X[x][d] Own[own][d] for the 16 rows starting at ``row0`` (multiple of 16).
 template <typename T, int DP>
 __device__ __forceinline__ void mma_d_sw(f32x4& acc, const unsigned char* region, int row0, const OwnFrag<T, DP>& f,
-                                         int l16, int g) {
-    const int row = row0 + l16;
+                                         const LaneOff<T, DP>& lo) {
+    const unsigned char* base = region + row0 * Sw<DP>::ROWB;
 #pragma unroll
     for (int c = 0; c < Lay<T, DP>::NC; ++c) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(region + Sw<DP>::off(row, 4 * c + g));
+        const u32x4 a = *reinterpret_cast<const u32x4*>(base + lo.a[c]);
         acc = ET<T>::mma(a, f.v[c], acc);
     }
 }
 
-// Seq-contraction A operand of d tile t for the 32 rows starting at x0, read transposed from the natural region.
+// Seq-contraction A operand of d tile t for the 32 rows starting at x0 (multiple of 32), read transposed.
 template <typename T, int DP>
-__device__ __forceinline__ SeqA<T> seqa_tr(const unsigned char* region, int x0, int t, int l16, int g) {
-    const int k = l16 >> 2, j = l16 & 3;
-    const int d = 16 * t + 4 * j;
-    const int c = d >> 3, inb = (d & 7) * 2;
-    const int xa = x0 + 4 * g + k;
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)(region + Sw<DP>::off(xa, c) + inb));
-    const s16x4 hi =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)(region + Sw<DP>::off(xa + 16, c) + inb));
-    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+__device__ __forceinline__ SeqA<T> seqa_tr(const unsigned char* region, int x0, int t, const LaneOff<T, DP>& lo) {
+    const unsigned char* base = region + x0 * Sw<DP>::ROWB + lo.tr[t];
+    const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)base);
+    const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)(base + 16 * Sw<DP>::ROWB));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo4), h2 = __builtin_bit_cast(u32x2, hi4);
     SeqA<T> a;
     a.v = u32x4{l2[0], l2[1], h2[0], h2[1]};
     return a;
@@ -100,25 +114,38 @@ template <int N> struct StatArrays {
     }
 };
 
+template <int C, int NCH, class F> __device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (C < NCH) {
+        f(std::integral_constant<int, C>{});
+        static_for<C + 1, NCH>(f);
+    }
+}
+
+// P tile of a row pass (own = queries, exponent scale folded: sc2 = scale * log2 e, lse2 = lse * log2 e); keys past
+// L are masked, which only the last chunk (LAST) can contain.
+template <bool LAST>
+__device__ __forceinline__ float row_p(float qk, float sc2, float lse2, int x, int L) {
+    const float pv = fast_exp2(fmaf(qk, sc2, -lse2));
+    if constexpr (LAST) return (x < L) ? pv : 0.f;
+    return pv;
+}
+
 // =====================================================================================================================
-// Forward
+// Forward: exact two-sweep softmax over the resident keys (the row maximum first, then exp, sum and P V).
 // =====================================================================================================================
 
-template <typename T, int DP> struct FwdRes {
-    static constexpr int SMEM = 2 * STAT_MAX * Sw<DP>::ROWB;  // K and V, up to 128 rows
-};
-
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd_res(Args a) {
+template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_fwd_res(Args a) {
     using LY = Lay<T, DP>;
-    __shared__ __align__(1024) unsigned char smem[FwdRes<T, DP>::SMEM];
+    constexpr int Lp = NCH * CH;
+    constexpr int RB = Lp * Sw<DP>::ROWB;
+    __shared__ __align__(1024) unsigned char smem[2 * RB];
     const WaveIds w = wave_ids();
     const int nw = w.nthr >> 6;
     const int bh = blockIdx.x;
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
-    const int Lp = (L + CH - 1) / CH * CH;
     unsigned char* Kr = smem;
-    unsigned char* Vr = smem + Lp * Sw<DP>::ROWB;
+    unsigned char* Vr = smem + RB;
     async_rows<T, DP>(Kr, slice<T>(a.k, b, h), a.k.sl, L, Lp, w.wave, nw, w.lane);
     async_rows<T, DP>(Vr, slice<T>(a.v, b, h), a.v.sl, L, Lp, w.wave, nw, w.lane);
     const int row0 = w.wave * 16;
@@ -126,46 +153,53 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd_res(A
     const bool active = row0 < L;
     OwnFrag<T, DP> qf;
     load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, DP, w.g);
+    const LaneOff<T, DP> lo(w.l16, w.g);
     async_wait();
     __syncthreads();
     if (!active) return;
-    const float sc = a.scale;
-    float m = -INFINITY, lsum = 0.f;
+    const float sc2 = a.scale * LOG2E;  // scores in log2 units
+    f32x4 s[2 * NCH];
+    float mx = -INFINITY;
+    static_for<0, NCH>([&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            mma_d_sw<T, DP>(v, Kr, C * CH + 16 * hh, qf, lo);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                v[r] *= sc2;
+                if constexpr (C == NCH - 1) {
+                    if (C * CH + 16 * hh + 4 * w.g + r >= L) v[r] = -INFINITY;
+                }
+                mx = fmaxf(mx, v[r]);
+            }
+            s[2 * C + hh] = v;
+        }
+    });
+    const float m = xmax4(mx);
+    float lsum = 0.f;
     f32x4 acc[LY::NT];
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int x0 = 0; x0 < L; x0 += CH) {
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
-        mma_d_sw<T, DP>(s0, Kr, x0, qf, w.l16, w.g);
-        mma_d_sw<T, DP>(s1, Kr, x0 + 16, qf, w.l16, w.g);
-        float mx = -INFINITY;
+    static_for<0, NCH>([&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+        f32x4 p0 = s[2 * C], p1 = s[2 * C + 1];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int x = x0 + 4 * w.g + r;
-            s0[r] = (x < L) ? s0[r] * sc : -INFINITY;
-            s1[r] = (x + 16 < L) ? s1[r] * sc : -INFINITY;
-            mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+            p0[r] = fast_exp2(p0[r] - m);
+            p1[r] = fast_exp2(p1[r] - m);
+            lsum += p0[r] + p1[r];
         }
-        const float mnew = fmaxf(m, xmax4(mx));
-        const float alpha = fast_exp2((m - mnew) * LOG2E);
-        float ps = 0.f;
+        const SeqB<T> pb = make_seqb<T>(p0, p1);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            s0[r] = fast_exp2((s0[r] - mnew) * LOG2E);
-            s1[r] = fast_exp2((s1[r] - mnew) * LOG2E);
-            ps += s0[r] + s1[r];
-        }
-        lsum = lsum * alpha + ps;
-        const SeqB<T> pb = make_seqb<T>(s0, s1);
-#pragma unroll
-        for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t] * alpha, seqa_tr<T, DP>(Vr, x0, t, w.l16, w.g), pb);
-        m = mnew;
-    }
+        for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Vr, C * CH, t, lo), pb);
+    });
     lsum = xsum4(lsum);
     if (own < L) {
         const int64_t r = (int64_t)bh * L + own;
         store_rows<T, DP>(a.out0, r * DP, acc, 1.f / lsum, DP, w.g);
-        if (w.g == 0) a.lse_out[r] = m + logf(lsum);
+        if (w.g == 0) a.lse_out[r] = m * (1.f / LOG2E) + logf(lsum);
     }
 }
 
@@ -173,28 +207,27 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd_res(A
 // Backward: row pass (dQ) then col pass (dK, dV) on one slice.
 // =====================================================================================================================
 
-template <typename T, int DP> struct BwdRes {
-    static constexpr int REGION = STAT_MAX * Sw<DP>::ROWB;           // one tensor, up to 128 rows
-    static constexpr bool SEP = 4 * REGION <= 64 * 1024;              // K, V, Q, dO all resident at once
-    static constexpr int SMEM = (SEP ? 4 : 2) * REGION;
+template <typename T, int DP, int NCH> struct BwdRes {
+    static constexpr int RB = NCH * CH * Sw<DP>::ROWB;  // one tensor
+    static constexpr bool SEP = 4 * RB <= 64 * 1024;     // K, V, Q, dO all resident at once
+    static constexpr int SMEM = (SEP ? 4 : 2) * RB;
 };
 
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_res(Args a) {
+template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bwd_res(Args a) {
     using LY = Lay<T, DP>;
-    using R = BwdRes<T, DP>;
+    using R = BwdRes<T, DP, NCH>;
+    constexpr int Lp = NCH * CH;
     __shared__ __align__(1024) unsigned char smem[R::SMEM];
-    __shared__ __align__(16) float st[2 * STAT_MAX];
+    __shared__ __align__(16) float st[2 * STAT_MAX];  // lse * log2 e, Dr
     const WaveIds w = wave_ids();
     const int nw = w.nthr >> 6;
     const int bh = blockIdx.x;
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
-    const int Lp = (L + CH - 1) / CH * CH;
-    const int rb = Lp * Sw<DP>::ROWB;
     unsigned char* Kr = smem;
-    unsigned char* Vr = smem + rb;
-    unsigned char* Qr = R::SEP ? smem + 2 * rb : smem;
-    unsigned char* Or = R::SEP ? smem + 3 * rb : smem + rb;  // dO
+    unsigned char* Vr = smem + R::RB;
+    unsigned char* Qr = R::SEP ? smem + 2 * R::RB : smem;
+    unsigned char* Or = R::SEP ? smem + 3 * R::RB : smem + R::RB;  // dO
     const T* Qg = slice<T>(a.q, b, h);
     const T* Og = slice<T>(a.dO, b, h);
     async_rows<T, DP>(Kr, slice<T>(a.k, b, h), a.k.sl, L, Lp, w.wave, nw, w.lane);
@@ -205,9 +238,11 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_res(A
     }
     StatArrays<2>{st}.defaults(w.tid, w.nthr);
     const float sc = a.scale;
+    const float sc2 = sc * LOG2E;
     const int row0 = w.wave * 16;
     const int own = row0 + w.l16;
     const bool active = row0 < L;
+    const LaneOff<T, DP> lo(w.l16, w.g);
 
     // ---- row pass: own = queries
     {
@@ -215,37 +250,39 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_res(A
         load_own<T, DP>(qf, Qg, a.q.sl, own, L, DP, w.g);
         load_own<T, DP>(df, Og, a.dO.sl, own, L, DP, w.g);
         load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
-        const float lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
+        const float lse2 = (own < L) ? a.lse[(int64_t)bh * L + own] * LOG2E : 0.f;
         const float dr = xsum4(frag_dot<T, DP>(df, of));
         async_wait();
         __syncthreads();  // regions loaded, statistics defaults written
         if (active) {
             if (w.g == 0) {
-                st[own] = (own < L) ? lse : INFINITY;
+                st[own] = (own < L) ? lse2 : INFINITY;
                 st[STAT_MAX + own] = (own < L) ? dr : 0.f;
             }
             f32x4 acc[LY::NT];
 #pragma unroll
             for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            for (int x0 = 0; x0 < L; x0 += CH) {
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                constexpr bool LAST = C == NCH - 1;
+                const int x0 = C * CH;
                 f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
-                mma_d_sw<T, DP>(p0, Kr, x0, qf, w.l16, w.g);
-                mma_d_sw<T, DP>(p1, Kr, x0 + 16, qf, w.l16, w.g);
-                mma_d_sw<T, DP>(d0, Vr, x0, df, w.l16, w.g);
-                mma_d_sw<T, DP>(d1, Vr, x0 + 16, df, w.l16, w.g);
+                mma_d_sw<T, DP>(p0, Kr, x0, qf, lo);
+                mma_d_sw<T, DP>(p1, Kr, x0 + 16, qf, lo);
+                mma_d_sw<T, DP>(d0, Vr, x0, df, lo);
+                mma_d_sw<T, DP>(d1, Vr, x0 + 16, df, lo);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int x = x0 + 4 * w.g + r;
-                    p0[r] = (x < L) ? fast_exp2(fmaf(p0[r], sc, -lse) * LOG2E) : 0.f;
-                    p1[r] = (x + 16 < L) ? fast_exp2(fmaf(p1[r], sc, -lse) * LOG2E) : 0.f;
+                    p0[r] = row_p<LAST>(p0[r], sc2, lse2, x, L);
+                    p1[r] = row_p<LAST>(p1[r], sc2, lse2, x + 16, L);
                     d0[r] = p0[r] * (d0[r] - dr);
                     d1[r] = p1[r] * (d1[r] - dr);
                 }
                 const SeqB<T> dsb = make_seqb<T>(d0, d1);
 #pragma unroll
-                for (int t = 0; t < LY::NT; ++t)
-                    acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, x0, t, w.l16, w.g), dsb);
-            }
+                for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, x0, t, lo), dsb);
+            });
             if (own < L) store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * DP, acc, sc, DP, w.g);
         }
     }
@@ -254,8 +291,8 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_res(A
     // ---- col pass: own = keys
     OwnFrag<T, DP> kf, vf;
     if (active) {
-        own_from_lds<T, DP>(kf, Kr, own, w.g);
-        own_from_lds<T, DP>(vf, Vr, own, w.g);
+        own_from_lds<T, DP>(kf, Kr, row0, lo);
+        own_from_lds<T, DP>(vf, Vr, row0, lo);
     }
     if constexpr (!R::SEP) {
         __syncthreads();  // every wave holds its K, V rows before Q, dO overwrite them
@@ -268,20 +305,22 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_res(A
     f32x4 ak[LY::NT], av[LY::NT];
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int x0 = 0; x0 < L; x0 += CH) {
+    static_for<0, NCH>([&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+        const int x0 = C * CH;
         const f32x4 l0 = *reinterpret_cast<const f32x4*>(st + x0 + 4 * w.g);
         const f32x4 l1 = *reinterpret_cast<const f32x4*>(st + x0 + 16 + 4 * w.g);
         const f32x4 r0 = *reinterpret_cast<const f32x4*>(st + STAT_MAX + x0 + 4 * w.g);
         const f32x4 r1 = *reinterpret_cast<const f32x4*>(st + STAT_MAX + x0 + 16 + 4 * w.g);
         f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
-        mma_d_sw<T, DP>(p0, Qr, x0, kf, w.l16, w.g);
-        mma_d_sw<T, DP>(p1, Qr, x0 + 16, kf, w.l16, w.g);
-        mma_d_sw<T, DP>(d0, Or, x0, vf, w.l16, w.g);
-        mma_d_sw<T, DP>(d1, Or, x0 + 16, vf, w.l16, w.g);
+        mma_d_sw<T, DP>(p0, Qr, x0, kf, lo);
+        mma_d_sw<T, DP>(p1, Qr, x0 + 16, kf, lo);
+        mma_d_sw<T, DP>(d0, Or, x0, vf, lo);
+        mma_d_sw<T, DP>(d1, Or, x0 + 16, vf, lo);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            p0[r] = fast_exp2(fmaf(p0[r], sc, -l0[r]) * LOG2E);
-            p1[r] = fast_exp2(fmaf(p1[r], sc, -l1[r]) * LOG2E);
+            p0[r] = fast_exp2(fmaf(p0[r], sc2, -l0[r]));  // lse = +inf on padded query rows -> P = 0
+            p1[r] = fast_exp2(fmaf(p1[r], sc2, -l1[r]));
             d0[r] = p0[r] * (d0[r] - r0[r]);
             d1[r] = p1[r] * (d1[r] - r1[r]);
         }
@@ -289,10 +328,10 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_res(A
         const SeqB<T> dsb = make_seqb<T>(d0, d1);
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) {
-            av[t] = mma_seq<T>(av[t], seqa_tr<T, DP>(Or, x0, t, w.l16, w.g), pb);
-            ak[t] = mma_seq<T>(ak[t], seqa_tr<T, DP>(Qr, x0, t, w.l16, w.g), dsb);
+            av[t] = mma_seq<T>(av[t], seqa_tr<T, DP>(Or, x0, t, lo), pb);
+            ak[t] = mma_seq<T>(ak[t], seqa_tr<T, DP>(Qr, x0, t, lo), dsb);
         }
-    }
+    });
     if (own < L) {
         const int64_t r = ((int64_t)bh * L + own) * DP;
         store_rows<T, DP>(a.out1, r, ak, sc, DP, w.g);
@@ -308,27 +347,28 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bwd_res(A
 // =====================================================================================================================
 
 template <typename T, int DP, int NCH> struct BbRes {
-    static constexpr int SMEM = 4 * NCH * CH * Sw<DP>::ROWB;  // K, gK, V, gV; later Q, gQ, dO in the same space
+    static constexpr int RB = NCH * CH * Sw<DP>::ROWB;
+    static constexpr int SMEM = 4 * RB;  // K, gK, V, gV; later Q, gQ, dO in the same space
 };
 
 template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bb_res(Args a) {
     using LY = Lay<T, DP>;
-    __shared__ __align__(1024) unsigned char smem[BbRes<T, DP, NCH>::SMEM];
-    __shared__ __align__(16) float st[4 * STAT_MAX];
+    using R = BbRes<T, DP, NCH>;
+    constexpr int Lp = NCH * CH;
+    __shared__ __align__(1024) unsigned char smem[R::SMEM];
+    __shared__ __align__(16) float st[4 * STAT_MAX];  // lse * log2 e, Dr, E, T
     const WaveIds w = wave_ids();
     const int nw = w.nthr >> 6;
     const int bh = blockIdx.x;
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
-    constexpr int Lp = NCH * CH;
-    constexpr int rb = Lp * Sw<DP>::ROWB;
     unsigned char* Kr = smem;
-    unsigned char* gKr = smem + rb;
-    unsigned char* Vr = smem + 2 * rb;
-    unsigned char* gVr = smem + 3 * rb;
+    unsigned char* gKr = smem + R::RB;
+    unsigned char* Vr = smem + 2 * R::RB;
+    unsigned char* gVr = smem + 3 * R::RB;
     unsigned char* Qr = smem;
-    unsigned char* gQr = smem + rb;
-    unsigned char* Or = smem + 2 * rb;  // dO
+    unsigned char* gQr = smem + R::RB;
+    unsigned char* Or = smem + 2 * R::RB;  // dO
     const T* Qg = slice<T>(a.q, b, h);
     const T* gQg = slice<T>(a.gq, b, h);
     const T* Og = slice<T>(a.dO, b, h);
@@ -338,9 +378,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     async_rows<T, DP>(gVr, slice<T>(a.gv, b, h), a.gv.sl, L, Lp, w.wave, nw, w.lane);
     StatArrays<4>{st}.defaults(w.tid, w.nthr);
     const float sc = a.scale;
+    const float sc2 = sc * LOG2E;
     const int row0 = w.wave * 16;
     const int own = row0 + w.l16;
     const bool active = row0 < L;
+    const LaneOff<T, DP> lo(w.l16, w.g);
 
     // ---- row pass: own = queries
     {
@@ -349,34 +391,34 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         load_own<T, DP>(gqf, gQg, a.gq.sl, own, L, DP, w.g);
         load_own<T, DP>(df, Og, a.dO.sl, own, L, DP, w.g);
         load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
-        const float lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
+        const float lse2 = (own < L) ? a.lse[(int64_t)bh * L + own] * LOG2E : 0.f;
         const float dr = xsum4(frag_dot<T, DP>(df, of));
         async_wait();
         __syncthreads();
         if (active) {
             SeqB<T> m1b[NCH], dsb[NCH], pb[NCH], pab[NCH];
             float e_acc = 0.f, t_acc = 0.f;
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const int x0 = c * CH;
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                constexpr bool LAST = C == NCH - 1;
+                const int x0 = C * CH;
                 f32x4 p[2], dp[2], at[2], bm[2];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
                     const int r0 = x0 + 16 * hh;
-                    mma_d_sw<T, DP>(p[hh], Kr, r0, qf, w.l16, w.g);
-                    mma_d_sw<T, DP>(at[hh], Kr, r0, gqf, w.l16, w.g);
-                    mma_d_sw<T, DP>(at[hh], gKr, r0, qf, w.l16, w.g);
-                    mma_d_sw<T, DP>(dp[hh], Vr, r0, df, w.l16, w.g);
-                    mma_d_sw<T, DP>(bm[hh], gVr, r0, df, w.l16, w.g);
+                    mma_d_sw<T, DP>(p[hh], Kr, r0, qf, lo);
+                    mma_d_sw<T, DP>(at[hh], Kr, r0, gqf, lo);
+                    mma_d_sw<T, DP>(at[hh], gKr, r0, qf, lo);
+                    mma_d_sw<T, DP>(dp[hh], Vr, r0, df, lo);
+                    mma_d_sw<T, DP>(bm[hh], gVr, r0, df, lo);
                 }
                 f32x4 ds[2], pa[2], m1[2];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int x = x0 + 16 * hh + 4 * w.g + r;
-                        const float pv = (x < L) ? fast_exp2(fmaf(p[hh][r], sc, -lse) * LOG2E) : 0.f;
+                        const float pv = row_p<LAST>(p[hh][r], sc2, lse2, x0 + 16 * hh + 4 * w.g + r, L);
                         const float dsv = pv * (dp[hh][r] - dr);
                         const float av = at[hh][r] * sc;
                         p[hh][r] = pv;
@@ -387,24 +429,24 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                         t_acc += m1[hh][r];
                     }
                 }
-                pb[c] = make_seqb<T>(p[0], p[1]);
-                dsb[c] = make_seqb<T>(ds[0], ds[1]);
-                pab[c] = make_seqb<T>(pa[0], pa[1]);
-                m1b[c] = make_seqb<T>(m1[0], m1[1]);
-            }
+                pb[C] = make_seqb<T>(p[0], p[1]);
+                dsb[C] = make_seqb<T>(ds[0], ds[1]);
+                pab[C] = make_seqb<T>(pa[0], pa[1]);
+                m1b[C] = make_seqb<T>(m1[0], m1[1]);
+            });
             const float E = xsum4(e_acc);
             const float Tm = xsum4(t_acc);
             f32x4 hq[LY::NT], hdo[LY::NT];
 #pragma unroll
             for (int t = 0; t < LY::NT; ++t) hq[t] = hdo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const int x0 = c * CH;
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                const int x0 = C * CH;
                 float m1f[8], dsf[8], pf[8], paf[8], d2[8], pe[8];
-                unpack_seqb<T>(m1b[c], m1f);
-                unpack_seqb<T>(dsb[c], dsf);
-                unpack_seqb<T>(pb[c], pf);
-                unpack_seqb<T>(pab[c], paf);
+                unpack_seqb<T>(m1b[C], m1f);
+                unpack_seqb<T>(dsb[C], dsf);
+                unpack_seqb<T>(pb[C], pf);
+                unpack_seqb<T>(pab[C], paf);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     d2[e] = m1f[e] - E * dsf[e] - Tm * pf[e];
@@ -414,12 +456,12 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 const SeqB<T> peb = pack_seqb<T>(pe);
 #pragma unroll
                 for (int t = 0; t < LY::NT; ++t) {
-                    hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(Kr, x0, t, w.l16, w.g), d2b);
-                    hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, w.l16, w.g), dsb[c]);
-                    hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(Vr, x0, t, w.l16, w.g), peb);
-                    hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, w.l16, w.g), pb[c]);
+                    hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(Kr, x0, t, lo), d2b);
+                    hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, lo), dsb[C]);
+                    hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(Vr, x0, t, lo), peb);
+                    hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, lo), pb[C]);
                 }
-            }
+            });
             if (own < L) {
                 const int64_t r = ((int64_t)bh * L + own) * DP;
                 store_rows<T, DP>(a.out0, r, hq, sc, DP, w.g);
@@ -427,7 +469,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             }
             if (w.g == 0) {
                 const bool ok = own < L;
-                st[own] = ok ? lse : INFINITY;
+                st[own] = ok ? lse2 : INFINITY;
                 st[STAT_MAX + own] = ok ? dr : 0.f;
                 st[2 * STAT_MAX + own] = ok ? E : 0.f;
                 st[3 * STAT_MAX + own] = ok ? Tm : 0.f;
@@ -439,10 +481,10 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     // ---- col pass: own = keys
     OwnFrag<T, DP> kf, gkf, vf, gvf;
     if (active) {
-        own_from_lds<T, DP>(kf, Kr, own, w.g);
-        own_from_lds<T, DP>(gkf, gKr, own, w.g);
-        own_from_lds<T, DP>(vf, Vr, own, w.g);
-        own_from_lds<T, DP>(gvf, gVr, own, w.g);
+        own_from_lds<T, DP>(kf, Kr, row0, lo);
+        own_from_lds<T, DP>(gkf, gKr, row0, lo);
+        own_from_lds<T, DP>(vf, Vr, row0, lo);
+        own_from_lds<T, DP>(gvf, gVr, row0, lo);
     }
     __syncthreads();  // every wave holds its key rows before Q, gQ, dO overwrite the regions
     async_rows<T, DP>(Qr, Qg, a.q.sl, L, Lp, w.wave, nw, w.lane);
@@ -454,17 +496,19 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     f32x4 hk[LY::NT], hv[LY::NT];
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int x0 = 0; x0 < L; x0 += CH) {
+    static_for<0, NCH>([&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+        const int x0 = C * CH;
         f32x4 p[2], dp[2], at[2], bm[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
             const int r0 = x0 + 16 * hh;
-            mma_d_sw<T, DP>(p[hh], Qr, r0, kf, w.l16, w.g);
-            mma_d_sw<T, DP>(at[hh], Qr, r0, gkf, w.l16, w.g);
-            mma_d_sw<T, DP>(at[hh], gQr, r0, kf, w.l16, w.g);
-            mma_d_sw<T, DP>(dp[hh], Or, r0, vf, w.l16, w.g);
-            mma_d_sw<T, DP>(bm[hh], Or, r0, gvf, w.l16, w.g);
+            mma_d_sw<T, DP>(p[hh], Qr, r0, kf, lo);
+            mma_d_sw<T, DP>(at[hh], Qr, r0, gkf, lo);
+            mma_d_sw<T, DP>(at[hh], gQr, r0, kf, lo);
+            mma_d_sw<T, DP>(dp[hh], Or, r0, vf, lo);
+            mma_d_sw<T, DP>(bm[hh], Or, r0, gvf, lo);
         }
         f32x4 ds[2], ds2[2], pa[2];
 #pragma unroll
@@ -476,7 +520,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             const f32x4 ts = *reinterpret_cast<const f32x4*>(st + 3 * STAT_MAX + so);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float pv = fast_exp2(fmaf(p[hh][r], sc, -ls[r]) * LOG2E);
+                const float pv = fast_exp2(fmaf(p[hh][r], sc2, -ls[r]));
                 const float dsv = pv * (dp[hh][r] - rs[r]);
                 const float av = at[hh][r] * sc;
                 ds[hh][r] = dsv;
@@ -490,11 +534,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         const SeqB<T> pab = make_seqb<T>(pa[0], pa[1]);
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) {
-            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, x0, t, w.l16, w.g), ds2b);
-            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, x0, t, w.l16, w.g), dsb);
-            hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, x0, t, w.l16, w.g), pab);
+            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, x0, t, lo), ds2b);
+            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, x0, t, lo), dsb);
+            hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, x0, t, lo), pab);
         }
-    }
+    });
     if (own < L) {
         const int64_t r = ((int64_t)bh * L + own) * DP;
         store_rows<T, DP>(a.out1, r, hk, sc, DP, w.g);

@@ -832,7 +832,13 @@ template <typename T, int DP> struct FwdLaunch {
         if constexpr (!ET<T>::F32) {
             if (resident_shape(a, DP, 2, false)) {
                 a.nblk = 1;
-                hipLaunchKernelGGL((k_fwd_res<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
+                const dim3 grid((int)bh), block(fused_threads(a.L));
+                switch ((a.L + CH - 1) / CH) {
+                    case 1: hipLaunchKernelGGL((k_fwd_res<T, DP, 1>), grid, block, 0, s, a); break;
+                    case 2: hipLaunchKernelGGL((k_fwd_res<T, DP, 2>), grid, block, 0, s, a); break;
+                    case 3: hipLaunchKernelGGL((k_fwd_res<T, DP, 3>), grid, block, 0, s, a); break;
+                    default: hipLaunchKernelGGL((k_fwd_res<T, DP, 4>), grid, block, 0, s, a); break;
+                }
                 return launch_rc();
             }
         }
@@ -857,7 +863,13 @@ template <typename T, int DP> struct BwdLaunch {
             a.gq = a.gk = a.gv = a.dO;  // only q, k, v, dO are read
             if (resident_shape(a, DP, 2, true)) {
                 a.nblk = 1;
-                hipLaunchKernelGGL((k_bwd_res<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
+                const dim3 grid((int)bh), block(fused_threads(a.L));
+                switch ((a.L + CH - 1) / CH) {
+                    case 1: hipLaunchKernelGGL((k_bwd_res<T, DP, 1>), grid, block, 0, s, a); break;
+                    case 2: hipLaunchKernelGGL((k_bwd_res<T, DP, 2>), grid, block, 0, s, a); break;
+                    case 3: hipLaunchKernelGGL((k_bwd_res<T, DP, 3>), grid, block, 0, s, a); break;
+                    default: hipLaunchKernelGGL((k_bwd_res<T, DP, 4>), grid, block, 0, s, a); break;
+                }
                 return launch_rc();
             }
         }
