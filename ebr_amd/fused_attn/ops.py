@@ -223,6 +223,8 @@ class _FusedAttnBwd(torch.autograd.Function):
         q, k, v, o, lse, do, scale = inputs
         ctx.save_for_backward(q, k, v, o, lse, do, output[0])
         ctx.scale = scale
+        # Unused outputs arrive as None (not as materialised zero tensors) and become expanded zero rows below.
+        ctx.set_materialize_grads(False)
 
     @staticmethod
     def backward(ctx, gq, gk, gv):

@@ -1,0 +1,284 @@
+"""Pins the CPU oracle (oracle/attention_ref.py) without retyping its formulas.
+
+- attn_fwd: torch.softmax / logsumexp closed forms, SDPA, and known answers (L = 1, Q = 0, key row shift, key/value
+  permutation, query permutation, rows of P summing to 1).
+- attn_bwd: the VJP of torch's SDPA and of autograd through the eager softmax attention; linearity in dO;
+  rowsum(dO * O) = rowsum(P * dP).
+- attn_bwd_bwd: autograd double backward through the eager attention (create_graph), central finite differences of
+  the first-order oracle (O and lse recomputed at each point), fp64 gradgradcheck, linearity in the cotangents and the
+  zero-cotangent special cases.
+A planted mistake (one dropped term) is shown to fail these checks.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from oracle import attention_ref as ref
+
+F64 = torch.float64
+
+
+def _rand(*shape, seed=0, dtype=F64, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=dtype) * scale
+
+
+def _qkv(B=2, H=3, L=7, D=8, seed=0):
+    return [_rand(B, H, L, D, seed=seed + i, scale=0.7) for i in range(7)]
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# forward
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+def test_fwd_matches_softmax_and_sdpa():
+    q, k, v, *_ = _qkv()
+    s = 0.3
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    scores = (q @ k.transpose(-1, -2)) * s
+    assert torch.allclose(o, torch.softmax(scores, -1) @ v, atol=1e-13)
+    assert torch.allclose(lse, torch.logsumexp(scores, -1), atol=1e-13)
+    o2 = F.scaled_dot_product_attention(q, k, v, scale=s)
+    assert torch.allclose(o, o2, atol=1e-12)
+    assert lse.dtype == F64 and o.dtype == F64
+
+
+def test_fwd_known_answers():
+    q, k, v, *_ = _qkv(L=1)
+    o, lse = oracle.attn_fwd(q, k, v, 0.5)
+    assert torch.equal(o, v)
+    assert torch.allclose(lse, 0.5 * (q * k).sum(-1), atol=1e-14)
+    q, k, v, *_ = _qkv(L=9)
+    o, lse = oracle.attn_fwd(torch.zeros_like(q), k, v, 0.5)
+    assert torch.allclose(o, v.mean(-2, keepdim=True).expand_as(v), atol=1e-14)
+    assert torch.allclose(lse, torch.full_like(lse, math.log(9)), atol=1e-14)
+
+
+def test_fwd_row_shift_and_permutations():
+    q, k, v, *_ = _qkv(L=11)
+    s = 0.25
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    u = _rand(1, 1, 1, q.shape[-1], seed=99)
+    o2, lse2 = oracle.attn_fwd(q, k + u, v, s)  # adds s * q.u to every score of a row
+    assert torch.allclose(o, o2, atol=1e-12)
+    assert torch.allclose(lse2, lse + s * (q * u).sum(-1), atol=1e-12)
+    perm = torch.randperm(11, generator=torch.Generator().manual_seed(3))
+    o3, lse3 = oracle.attn_fwd(q, k[:, :, perm], v[:, :, perm], s)
+    assert torch.allclose(o, o3, atol=1e-12) and torch.allclose(lse, lse3, atol=1e-12)
+    o4, _ = oracle.attn_fwd(q[:, :, perm], k, v, s)
+    assert torch.allclose(o[:, :, perm], o4, atol=1e-12)
+
+
+def test_fwd_rows_of_p_sum_to_one():
+    L = 6
+    q, k, *_ = _qkv(L=L, D=L)
+    eye = torch.eye(L, dtype=F64).expand(2, 3, L, L)
+    p, _ = oracle.attn_fwd(q, k, eye, 0.4)  # O = P I = P
+    assert torch.allclose(p.sum(-1), torch.ones(2, 3, L, dtype=F64), atol=1e-14)
+    assert (p >= 0).all()
+
+
+def test_fwd_dtype_rules():
+    q, k, v, *_ = _qkv()
+    o, lse = oracle.attn_fwd(q.bfloat16(), k.bfloat16(), v.bfloat16(), 0.3)
+    assert o.dtype == torch.bfloat16 and lse.dtype == torch.float32
+    o, lse = oracle.attn_fwd(q.float(), k.float(), v.float(), 0.3)
+    assert o.dtype == torch.float32 and lse.dtype == torch.float32
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# backward
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+def _sdpa_vjp(q, k, v, do, s):
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = F.scaled_dot_product_attention(qq, kk, vv, scale=s)
+    return torch.autograd.grad(o, (qq, kk, vv), do)
+
+
+@pytest.mark.parametrize("L", [1, 5, 16, 33])
+def test_bwd_matches_sdpa_vjp(L):
+    q, k, v, do, *_ = _qkv(L=L)
+    s = 0.35
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    got = oracle.attn_bwd(q, k, v, o, lse, do, s)
+    want = _sdpa_vjp(q, k, v, do, s)
+    for g_, w_ in zip(got, want):
+        assert torch.allclose(g_, w_, atol=1e-11)
+
+
+def test_bwd_matches_autograd_of_eager_attention():
+    q, k, v, do, *_ = _qkv(L=13, D=16)
+    o, lse = oracle.attn_fwd(q, k, v, 16**-0.5)
+    got = oracle.attn_bwd(q, k, v, o, lse, do, 16**-0.5)
+    want = oracle.autograd_bwd(q, k, v, do)
+    for g_, w_ in zip(got, want):
+        assert torch.allclose(g_, w_, atol=1e-11)
+
+
+def test_bwd_linear_in_do_and_dr_identity():
+    q, k, v, do, r1, *_ = _qkv(L=9)
+    s = 0.3
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    a = oracle.attn_bwd(q, k, v, o, lse, do, s)
+    b = oracle.attn_bwd(q, k, v, o, lse, r1, s)
+    c = oracle.attn_bwd(q, k, v, o, lse, 2 * do - 3 * r1, s)
+    for x, y, z in zip(a, b, c):
+        assert torch.allclose(z, 2 * x - 3 * y, atol=1e-12)
+    p = torch.softmax((q @ k.transpose(-1, -2)) * s, -1)
+    dp = do @ v.transpose(-1, -2)
+    assert torch.allclose((do * o).sum(-1), (p * dp).sum(-1), atol=1e-12)
+
+
+def test_bwd_gradcheck_fp64():
+    q, k, v, do, *_ = _qkv(B=1, H=2, L=4, D=3)
+    s = 0.6
+
+    def f(q, k, v):
+        return F.scaled_dot_product_attention(q, k, v, scale=s)
+
+    ins = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    assert torch.autograd.gradcheck(f, ins)
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    got = oracle.attn_bwd(q, k, v, o, lse, do, s)
+    want = torch.autograd.grad(f(*ins), ins, do)
+    for g_, w_ in zip(got, want):
+        assert torch.allclose(g_, w_, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# backward of the backward
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+def _bb(q, k, v, do, gq, gk, gv, s):
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    dq, _, _ = oracle.attn_bwd(q, k, v, o, lse, do, s)
+    return oracle.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, s)
+
+
+@pytest.mark.parametrize("L,D", [(1, 4), (6, 8), (17, 16), (40, 8)])
+def test_bwd_bwd_matches_autograd_double_backward(L, D):
+    q, k, v, do, gq, gk, gv = _qkv(L=L, D=D, seed=L)
+    got = _bb(q, k, v, do, gq, gk, gv, D**-0.5)
+    want = oracle.autograd_bwd_bwd(q, k, v, do, gq, gk, gv)
+    for g_, w_ in zip(got, want):
+        assert torch.allclose(g_, w_, atol=1e-11), (g_ - w_).abs().max()
+
+
+def _phi(q, k, v, do, gq, gk, gv, s):
+    o, lse = oracle.attn_fwd(q, k, v, s)  # recomputed: the total derivative includes o's and lse's dependence
+    dq, dk, dv = oracle.attn_bwd(q, k, v, o, lse, do, s)
+    return (dq * gq).sum() + (dk * gk).sum() + (dv * gv).sum()
+
+
+def test_bwd_bwd_central_differences():
+    q, k, v, do, gq, gk, gv = _qkv(L=7, D=5, seed=4)
+    s = 0.45
+    h = _bb(q, k, v, do, gq, gk, gv, s)
+    eps = 1e-5
+    for i in range(4):  # perturb q, k, v, dO in turn along a random direction
+        delta = _rand(*q.shape, seed=50 + i)
+        xs_p = [q, k, v, do]
+        xs_m = [q, k, v, do]
+        xs_p = [x + eps * delta if j == i else x for j, x in enumerate(xs_p)]
+        xs_m = [x - eps * delta if j == i else x for j, x in enumerate(xs_m)]
+        fd = (_phi(*xs_p, gq, gk, gv, s) - _phi(*xs_m, gq, gk, gv, s)) / (2 * eps)
+        an = (h[i] * delta).sum()
+        assert abs(float(fd - an)) <= 1e-7 * max(1.0, abs(float(an))), (i, float(fd), float(an))
+
+
+def test_eager_attention_gradgradcheck():
+    q, k, v, *_ = _qkv(B=1, H=1, L=4, D=3)
+    ins = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    assert torch.autograd.gradgradcheck(oracle.math_attention, ins)
+
+
+def test_bwd_bwd_special_cases_and_linearity():
+    q, k, v, do, gq, gk, gv = _qkv(L=9, D=8, seed=7)
+    s = 8**-0.5
+    z = torch.zeros_like(q)
+    for t in _bb(q, k, v, do, z, z, z, s):
+        assert torch.equal(t, torch.zeros_like(t))
+    hq, hk, hv, hdo = _bb(q, k, v, do, z, z, gv, s)
+    p = torch.softmax((q @ k.transpose(-1, -2)) * s, -1)
+    assert torch.allclose(hv, torch.zeros_like(hv), atol=1e-14)
+    assert torch.allclose(hdo, p @ gv, atol=1e-12)
+    a = _bb(q, k, v, do, gq, gk, gv, s)
+    b = _bb(q, k, v, do, do, gq, gk, s)
+    c = _bb(q, k, v, do, 2 * gq - do, 2 * gk - gq, 2 * gv - gk, s)
+    for x, y, w_ in zip(a, b, c):
+        assert torch.allclose(w_, 2 * x - y, atol=1e-11)
+
+
+def test_bwd_bwd_ignores_dq_and_casts_cotangents():
+    q, k, v, do, gq, gk, gv = _qkv(L=5, seed=2)
+    s = 0.3
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    a = oracle.attn_bwd_bwd(q, k, v, o, lse, do, None, gq, gk, gv, s)
+    b = oracle.attn_bwd_bwd(q, k, v, o, lse, do, torch.full_like(q, 1e9), gq, gk, gv, s)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_planted_mistake_is_caught(monkeypatch):
+    """A 0.1% error planted in the oracle's dS makes the autograd comparison fail (the check has teeth)."""
+    q, k, v, do, gq, gk, gv = _qkv(L=6, D=4, seed=12)
+    s = 4**-0.5  # the eager attention's scale for D = 4
+    want = oracle.autograd_bwd_bwd(q, k, v, do, gq, gk, gv)
+    good = _bb(q, k, v, do, gq, gk, gv, s)
+    assert all(torch.allclose(x, y, atol=1e-11) for x, y in zip(good, want))
+    real_first = ref._first_order
+
+    def broken_first(*args):
+        p, dp, dr, ds = real_first(*args)
+        return p, dp, dr, ds * 1.001
+
+    monkeypatch.setattr(ref, "_first_order", broken_first)
+    bad = _bb(q, k, v, do, gq, gk, gv, s)
+    assert any(not torch.allclose(x, y, atol=1e-9) for x, y in zip(bad, want))
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# BASELINE config 0 (fp32, B=32 H=8 L=64 D=64) and the chunked path
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+def test_config0_fp32_oracle_within_1e5_of_fp64():
+    q, k, v, do, r1, r2, r3 = oracle.make_inputs(32, 8, 64, 64, dtype=torch.float32, seed=0)
+    s = 64**-0.5
+    o32, lse32 = oracle.attn_fwd(q, k, v, s)
+    d32 = oracle.attn_bwd(q, k, v, o32, lse32, do, s)
+    h32 = oracle.attn_bwd_bwd(q, k, v, o32, lse32, do, None, r1, r2, r3, s)
+    q64, k64, v64, do64, g1, g2, g3 = (t.double() for t in (q, k, v, do, r1, r2, r3))
+    o64, lse64 = oracle.attn_fwd(q64, k64, v64, s)
+    d64 = oracle.attn_bwd(q64, k64, v64, o64, lse64, do64, s)
+    h64 = oracle.attn_bwd_bwd(q64, k64, v64, o64, lse64, do64, None, g1, g2, g3, s)
+    for a, b in zip([o32, lse32, *d32, *h32], [o64, lse64, *d64, *h64]):
+        assert oracle.rel_err(a, b) < 1e-5
+
+
+def test_chunking_changes_nothing():
+    q, k, v, do, gq, gk, gv = _qkv(B=3, H=5, L=9, D=4, seed=8)
+    s = 0.4
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    o2, lse2 = oracle.attn_fwd(q, k, v, s, chunk=4)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    a = oracle.attn_bwd_bwd(q, k, v, o, lse, do, None, gq, gk, gv, s)
+    b = oracle.attn_bwd_bwd(q, k, v, o, lse, do, None, gq, gk, gv, s, chunk=2)
+    for x, y in zip(a, b):
+        assert torch.allclose(x, y, atol=1e-14)
+
+
+def test_make_inputs_recipe():
+    a = oracle.make_inputs(2, 2, 3, 4, dtype=torch.bfloat16, seed=0, qkv_scale=0.125)
+    g = torch.Generator().manual_seed(0)
+    first = torch.randn((2, 2, 3, 4), generator=g)
+    assert torch.equal(a[0], (first * 0.125).bfloat16())
+    assert all(t.dtype == torch.bfloat16 for t in a) and len(a) == 7
