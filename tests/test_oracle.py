@@ -282,3 +282,11 @@ def test_make_inputs_recipe():
     first = torch.randn((2, 2, 3, 4), generator=g)
     assert torch.equal(a[0], (first * 0.125).bfloat16())
     assert all(t.dtype == torch.bfloat16 for t in a) and len(a) == 7
+
+
+def test_package_input_recipe_matches_oracle_recipe():
+    from ebr_amd.workloads import seeded_inputs
+
+    a = seeded_inputs(3, 2, 5, 8, dtype=torch.bfloat16, seed=4, qkv_scale=0.125)
+    b = oracle.make_inputs(3, 2, 5, 8, dtype=torch.bfloat16, seed=4, qkv_scale=0.125)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
