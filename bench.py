@@ -268,8 +268,103 @@ def pmc_target(cfg: dict, reps: int = 3) -> None:
         log(f"pmc target: {p} algorithmic bytes per launch {roofline.phase_bytes(p, B, H, L, D, es):.0f}")
 
 
+def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
+    """BASELINE config 3: 2 post-norm blocks, hidden 512, 8 x 64 heads, SwiGLU x4, mean-pooled linear energy head;
+    x ~ U{0..10} [384, 81]; z ~ N(0, 1) [384, 81, 512]; 16 steps z <- z - 0.1 dE/dz with create_graph; CE of a linear
+    decode head to random targets; backward; bf16. GPU: the fused (gfx950) attention. CPU: the same step with the eager
+    'math' attention on the host's cores, at batch ``cpu_sample_b``, scaled linearly to batch 384."""
+    from ebr_amd import energy as en
+
+    B, L, V = 384, 81, 11
+    dev = torch.device("cuda", 0)
+    cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused")
+    model, dec = en.build(cfg, dev)
+    g = torch.Generator("cpu").manual_seed(0)
+    x = torch.randint(0, V, (B, L), generator=g).to(dev)
+    z0 = torch.randn(B, L, cfg.hidden_size, generator=g).to(dev, torch.bfloat16)
+    tg = torch.randint(0, V, (B, L), generator=g).to(dev)
+    for _ in range(warmup):
+        en.train_step(model, dec, x, z0, tg)
+        model.zero_grad(set_to_none=True)
+        dec.zero_grad(set_to_none=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        loss = en.train_step(model, dec, x, z0, tg)
+        model.zero_grad(set_to_none=True)
+        dec.zero_grad(set_to_none=True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    out = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 2), "loss": round(float(loss), 4),
+           "config": "B=384 L=81 hidden=512 heads=8x64 layers=2 SwiGLU x4, 16 create_graph descent steps, bf16",
+           "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 2**30, 1)}
+    if cpu_sample_b > 0:
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        ccfg = en.EnergyConfig(attn_backend="math", attn_nograd_backend="math")
+        cm, cd = en.build(ccfg, torch.device("cpu"))
+        cx, cz, ct = x[:cpu_sample_b].cpu(), z0[:cpu_sample_b].cpu(), tg[:cpu_sample_b].cpu()
+        en.train_step(cm, cd, cx, cz, ct)  # warm-up (and the second-order self-test)
+        times = []
+        for _ in range(2):
+            cm.zero_grad(set_to_none=True)
+            t = time.perf_counter()
+            en.train_step(cm, cd, cx, cz, ct)
+            times.append(time.perf_counter() - t)
+        sec = min(times) * B / cpu_sample_b
+        out["cpu"] = {"steps_per_s": round(1.0 / sec, 5), "cores": cores, "kind": "port",
+                      "sample": f"the same step with the eager math attention at batch {cpu_sample_b} (of {B}), "
+                      f"best of 2 after 1 warm-up, scaled linearly to batch {B}"}
+        out["speedup_vs_cpu"] = round(out["steps_per_s"] / out["cpu"]["steps_per_s"], 1)
+    return out
+
+
+def ebr_infer(cpu_sample_n: int):
+    """256 inputs x 20 samples = 5120 sequences of L = 100 (10 x 10), same architecture, 64 descent
+    steps of dE/dz without a graph (fwd + bwd), lowest-energy sample per input; bf16. The CPU time runs
+    ``cpu_sample_n`` sequences for 2 steps and is scaled linearly to 5120 sequences and 64 steps."""
+    from ebr_amd import energy as en
+
+    N, S, L, V, STEPS = 256, 20, 100, 3, 64
+    dev = torch.device("cuda", 0)
+    cfg = en.EnergyConfig(grid=(10, 10), vocab_size=V)
+    model, _ = en.build(cfg, dev)
+    for p in model.parameters():
+        p.requires_grad_(False)
+    g = torch.Generator("cpu").manual_seed(0)
+    x = torch.randint(0, V, (N, L), generator=g).to(dev)
+    z0 = torch.randn(N * S, L, cfg.hidden_size, generator=g).to(dev, torch.bfloat16)
+    en.infer(model, x[:8], z0[: 8 * S], S, steps=2)  # warm-up
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    best, e = en.infer(model, x, z0, S, steps=STEPS)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t
+    out = {"seconds": round(sec, 3), "config": "5120 x L=100, 64 descent steps (fwd+bwd), bf16, argmin over 20 samples"}
+    if cpu_sample_n > 0:
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        ccfg = en.EnergyConfig(grid=(10, 10), vocab_size=V, attn_backend="math", attn_nograd_backend="math")
+        cm, _ = en.build(ccfg, torch.device("cpu"))
+        for p in cm.parameters():
+            p.requires_grad_(False)
+        n_in = max(1, cpu_sample_n // S)
+        en.infer(cm, x[:n_in].cpu(), z0[: n_in * S].cpu(), S, steps=1)
+        t = time.perf_counter()
+        en.infer(cm, x[:n_in].cpu(), z0[: n_in * S].cpu(), S, steps=2)
+        csec = (time.perf_counter() - t) / 2 * STEPS * (N / n_in)
+        out["cpu_seconds_extrapolated"] = round(csec, 1)
+        out["cpu_sample"] = f"{n_in * S} sequences x 2 steps, scaled linearly to 5120 sequences x 64 steps"
+        out["speedup_vs_cpu"] = round(csec / sec, 1)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--no-ebr", action="store_true", help="skip the EBR training-step measurement (config 3)")
+    ap.add_argument("--ebr-infer", action="store_true", help="also run the inference descent (config 4)")
+    ap.add_argument("--ebr-steps", type=int, default=3)
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -385,6 +480,14 @@ def main() -> int:
         out["parity_max_rel_err"] = float(f"{err:.3e}")
     else:
         out["cpu_baseline"] = None
+    if not args.no_ebr:
+        log("EBR training step (config 3)")
+        out["ebr_train"] = ebr_train(args.ebr_steps, 1, 0 if args.no_cpu else 8)
+        log(f"EBR train: {out['ebr_train']}")
+    if args.ebr_infer:
+        log("EBR inference descent (config 4)")
+        out["ebr_infer"] = ebr_infer(0 if args.no_cpu else 40)
+        log(f"EBR infer: {out['ebr_infer']}")
     print(json.dumps(out), flush=True)
     return 0
 

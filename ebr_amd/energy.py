@@ -1,0 +1,129 @@
+"""Energy network and latent descent: the harness BASELINE configurations 3 and 4 run the attention path through.
+
+Follows the reference's structure, restated at the size BASELINE names:
+- ``ScalarEnergy`` (models/energy.py:204-216): E(z; x) from ``num_layers`` post-norm blocks
+  (models/attention.py:248-266) over z + embed(x). BASELINE config 3 names a mean-pooled linear energy head, used
+  here instead of the reference's per-cell MLP head (models/energy.py:190-201).
+- ``energy_grad`` (models/energy.py:345-350): opens the second-order window when the graph is kept, runs the energy
+  forward and takes dE/dz with ``torch.autograd.grad`` (``create_graph`` for graded steps).
+- ``descend``: z <- z - alpha dE/dz for ``steps`` steps (the reference adds noise, rms_norm and a
+  sphere projection per microstep, models/energy.py:219-241, which config 3 does not ask for).
+- ``train_step`` (config 3): ``steps`` graded descent steps, a linear decode head, cross-entropy to targets, backward.
+- ``infer`` (config 4): descent without a graph over ``samples`` latents per input, then the lowest-energy sample per
+  input (evaluators/protocol.py:10-12).
+
+The attention backend is a parameter: ``fused`` (the gfx950 kernels) on the GPU; the CPU baseline passes ``math``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ebr_amd.attention import EnergyReasoningBlock, second_order_window
+from ebr_amd.layers import CastedLinear, RotaryEmbedding2D, trunc_normal_init_
+
+
+@dataclass
+class EnergyConfig:
+    hidden_size: int = 512
+    num_heads: int = 8
+    num_layers: int = 2
+    expansion: float = 4.0
+    vocab_size: int = 11
+    grid: tuple = (9, 9)  # board height x width; L = height * width
+    attn_backend: str = "fused"
+    attn_nograd_backend: str = "fused"
+    rope: bool = True
+
+
+class ScalarEnergy(nn.Module):
+    def __init__(self, cfg: EnergyConfig) -> None:
+        super().__init__()
+        self.cfg = cfg
+        self.embed = nn.Parameter(trunc_normal_init_(torch.empty(cfg.vocab_size, cfg.hidden_size), std=1.0))
+        self.layers = nn.ModuleList(EnergyReasoningBlock(cfg) for _ in range(cfg.num_layers))
+        self.energy_head = CastedLinear(cfg.hidden_size, 1, bias=False)
+        head_dim = cfg.hidden_size // cfg.num_heads
+        self.rope = RotaryEmbedding2D(head_dim, *cfg.grid) if cfg.rope else None
+
+    def puzzle_embedding(self, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        return F.embedding(x, self.embed.to(dtype))
+
+    def forward(self, z: torch.Tensor, x_emb: torch.Tensor) -> torch.Tensor:
+        """Energy per row, fp32 [B]."""
+        cos_sin = self.rope() if self.rope is not None else None
+        h = z + x_emb
+        for layer in self.layers:
+            h = layer(cos_sin, h)
+        return self.energy_head(h.mean(dim=1)).float().squeeze(-1)
+
+
+def energy_grad(model: ScalarEnergy, v: torch.Tensor, x_emb: torch.Tensor, create_graph: bool) -> torch.Tensor:
+    with second_order_window(create_graph):
+        e = model(v, x_emb)
+    (g,) = torch.autograd.grad(e.sum(), v, create_graph=create_graph)
+    return g
+
+
+def descend(model, z, x_emb, steps: int, alpha: float, create_graph: bool) -> torch.Tensor:
+    v = z if z.requires_grad else z.detach().requires_grad_(True)
+    for _ in range(steps):
+        g = energy_grad(model, v, x_emb, create_graph)
+        v = v - alpha * g
+        if not create_graph:
+            v = v.detach().requires_grad_(True)
+    return v
+
+
+class Decoder(nn.Module):
+    def __init__(self, cfg: EnergyConfig) -> None:
+        super().__init__()
+        self.lm_head = CastedLinear(cfg.hidden_size, cfg.vocab_size, bias=False)
+
+    def forward(self, v: torch.Tensor) -> torch.Tensor:
+        return self.lm_head(v).float()
+
+
+def train_step(model, decoder, x, z0, targets, steps: int = 16, alpha: float = 0.1) -> torch.Tensor:
+    """One config-3 training step: graded descent (create_graph), CE to ``targets``, backward. Returns the loss."""
+    x_emb = model.puzzle_embedding(x, z0.dtype)
+    z = z0.detach().requires_grad_(True)
+    v = descend(model, z, x_emb, steps, alpha, create_graph=True)
+    logits = decoder(v)
+    loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1))
+    loss.backward()
+    return loss.detach()
+
+
+@torch.no_grad()
+def _energies(model, v, x_emb):
+    return model(v, x_emb)
+
+
+def infer(model, x, z0, samples: int, steps: int = 64, alpha: float = 0.1):
+    """Config 4: ``x`` [N, L] inputs, ``z0`` [N * samples, L, hidden] latents; returns (best latent per input [N, L,
+    hidden], its energy [N])."""
+    n = x.shape[0]
+    xs = x.repeat_interleave(samples, dim=0)
+    with torch.no_grad():
+        x_emb = model.puzzle_embedding(xs, z0.dtype)
+    v = descend(model, z0, x_emb, steps, alpha, create_graph=False)
+    e = _energies(model, v, x_emb).view(n, samples)
+    best = e.argmin(dim=1)
+    idx = torch.arange(n, device=x.device) * samples + best
+    return v.detach()[idx], e.gather(1, best[:, None]).squeeze(1)
+
+
+def build(cfg: EnergyConfig, device: torch.device, seed: int = 0):
+    torch.manual_seed(seed)
+    model = ScalarEnergy(cfg).to(device)
+    decoder = Decoder(cfg).to(device)
+    return model, decoder
+
+
+__all__ = ["Decoder", "EnergyConfig", "ScalarEnergy", "build", "descend", "energy_grad", "infer", "train_step"]
