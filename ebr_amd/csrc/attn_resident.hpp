@@ -155,7 +155,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, DP, w.g);
     const LaneOff<T, DP> lo(w.l16, w.g);
     async_wait();
-    __syncthreads();
+    lds_barrier();
     if (!active) return;
     const float sc2 = a.scale * LOG2E;  // scores in log2 units
     f32x4 s[2 * NCH];
@@ -250,10 +250,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         load_own<T, DP>(qf, Qg, a.q.sl, own, L, DP, w.g);
         load_own<T, DP>(df, Og, a.dO.sl, own, L, DP, w.g);
         load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
-        const float lse2 = (own < L) ? a.lse[(int64_t)bh * L + own] * LOG2E : 0.f;
+        const float lraw = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)];  // unconditional load
+        const float lse2 = (own < L) ? lraw * LOG2E : 0.f;
         const float dr = xsum4(frag_dot<T, DP>(df, of));
         async_wait();
-        __syncthreads();  // regions loaded, statistics defaults written
+        lds_barrier();  // regions loaded, statistics defaults written
         if (active) {
             if (w.g == 0) {
                 st[own] = (own < L) ? lse2 : INFINITY;
@@ -286,7 +287,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             if (own < L) store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * DP, acc, sc, DP, w.g);
         }
     }
-    __syncthreads();  // statistics published; K, V no longer read by the row pass
+    lds_barrier();  // statistics published; K, V no longer read by the row pass
 
     // ---- col pass: own = keys
     OwnFrag<T, DP> kf, vf;
@@ -295,11 +296,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         own_from_lds<T, DP>(vf, Vr, row0, lo);
     }
     if constexpr (!R::SEP) {
-        __syncthreads();  // every wave holds its K, V rows before Q, dO overwrite them
+        lds_barrier();  // every wave holds its K, V rows before Q, dO overwrite them
         async_rows<T, DP>(Qr, Qg, a.q.sl, L, Lp, w.wave, nw, w.lane);
         async_rows<T, DP>(Or, Og, a.dO.sl, L, Lp, w.wave, nw, w.lane);
         async_wait();
-        __syncthreads();
+        lds_barrier();
     }
     if (!active) return;
     f32x4 ak[LY::NT], av[LY::NT];
@@ -391,10 +392,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         load_own<T, DP>(gqf, gQg, a.gq.sl, own, L, DP, w.g);
         load_own<T, DP>(df, Og, a.dO.sl, own, L, DP, w.g);
         load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
-        const float lse2 = (own < L) ? a.lse[(int64_t)bh * L + own] * LOG2E : 0.f;
+        const float lraw = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)];  // unconditional load
+        const float lse2 = (own < L) ? lraw * LOG2E : 0.f;
         const float dr = xsum4(frag_dot<T, DP>(df, of));
         async_wait();
-        __syncthreads();
+        lds_barrier();
         if (active) {
             SeqB<T> m1b[NCH], dsb[NCH], pb[NCH], pab[NCH];
             float e_acc = 0.f, t_acc = 0.f;
@@ -476,7 +478,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             }
         }
     }
-    __syncthreads();  // statistics published; the row pass no longer reads K, gK, V, gV
+    lds_barrier();  // statistics published; the row pass no longer reads K, gK, V, gV
 
     // ---- col pass: own = keys
     OwnFrag<T, DP> kf, gkf, vf, gvf;
@@ -486,12 +488,12 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         own_from_lds<T, DP>(vf, Vr, row0, lo);
         own_from_lds<T, DP>(gvf, gVr, row0, lo);
     }
-    __syncthreads();  // every wave holds its key rows before Q, gQ, dO overwrite the regions
+    lds_barrier();  // every wave holds its key rows before Q, gQ, dO overwrite the regions
     async_rows<T, DP>(Qr, Qg, a.q.sl, L, Lp, w.wave, nw, w.lane);
     async_rows<T, DP>(gQr, gQg, a.gq.sl, L, Lp, w.wave, nw, w.lane);
     async_rows<T, DP>(Or, Og, a.dO.sl, L, Lp, w.wave, nw, w.lane);
     async_wait();
-    __syncthreads();
+    lds_barrier();
     if (!active) return;
     f32x4 hk[LY::NT], hv[LY::NT];
 #pragma unroll
@@ -537,6 +539,220 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, x0, t, lo), ds2b);
             hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, x0, t, lo), dsb);
             hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, x0, t, lo), pab);
+        }
+    });
+    if (own < L) {
+        const int64_t r = ((int64_t)bh * L + own) * DP;
+        store_rows<T, DP>(a.out1, r, hk, sc, DP, w.g);
+        store_rows<T, DP>(a.out2, r, hv, 1.f, DP, w.g);
+    }
+}
+
+// =====================================================================================================================
+// Backward of the backward with the L x L tiles shared through LDS (16-bit inputs, D <= 64, L <= 96).
+// The row pass (as in k_bb_res) also writes its dS2, dS and Pa tiles, rounded to the input type, into LDS as
+// [query][key] rows. The col pass then needs neither the scores nor any elementwise work: with A = Q, gQ, dO read
+// transposed from their natural rows and B = the tiles read transposed (lane = key, k-slots = queries),
+//   hK = s (dS2^T Q + dS^T gQ),  hV = Pa^T dO
+// are 3 GEMM units: 12 for the whole backward of the backward, the minimum. Q, gQ, dO have their own region and
+// are loaded while the row pass runs. One wave per 16 rows covers every tile row (padded rows are written as 0).
+// =====================================================================================================================
+
+template <typename T, int DP, int NCH> struct BbShare {
+    static constexpr int LP = NCH * CH;
+    static constexpr int RB = LP * Sw<DP>::ROWB;  // one natural tensor region
+    static constexpr int TP = LP * 2 + 32;        // tile row pitch (bytes), padded off the 256-byte bank period
+    static constexpr int TB = LP * TP;            // one tile
+    static constexpr int SMEM = 7 * RB + 3 * TB;  // K, gK, V, gV | Q, gQ, dO | dS2, dS, Pa
+    static constexpr int NW = 2 * NCH;            // waves
+    // 1 KB buffer loads each wave issues for Q, gQ, dO (3 tensors x LP / RPI blocks over NW waves)
+    static constexpr int QLOADS = 3 * (LP / Sw<DP>::RPI) / NW;
+};
+
+// 8-byte tile write: row ``row`` (query), keys key0 .. key0 + 3 (4 packed 16-bit values).
+__device__ __forceinline__ void tile_store8(unsigned char* tile, int pitch, int row, int key0, u32x2 v) {
+    *reinterpret_cast<u32x2*>(tile + row * pitch + key0 * 2) = v;
+}
+
+// B operand of the col pass from a [query][key] tile: lane (key = kb + l16, group g), k-slot 4 h + k holds
+// tile[x0 + 16 h + 4 g + k][kb + l16].
+template <typename T>
+__device__ __forceinline__ SeqB<T> tile_seqb(const unsigned char* tile, int pitch, int x0, int kb, int l16, int g) {
+    const int k = l16 >> 2, j = l16 & 3;
+    const unsigned char* p = tile + (x0 + 4 * g + k) * pitch + (kb + 4 * j) * 2;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)p);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)(p + 16 * pitch));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    SeqB<T> b;
+    b.v = u32x4{l2[0], l2[1], h2[0], h2[1]};
+    return b;
+}
+
+template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bb_share(Args a) {
+    using LY = Lay<T, DP>;
+    using R = BbShare<T, DP, NCH>;
+    constexpr int Lp = R::LP;
+    __shared__ __align__(1024) unsigned char smem[R::SMEM];
+    const WaveIds w = wave_ids();
+    const int bh = blockIdx.x;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L;
+    unsigned char* Kr = smem;
+    unsigned char* gKr = smem + R::RB;
+    unsigned char* Vr = smem + 2 * R::RB;
+    unsigned char* gVr = smem + 3 * R::RB;
+    unsigned char* Qr = smem + 4 * R::RB;
+    unsigned char* gQr = smem + 5 * R::RB;
+    unsigned char* Or = smem + 6 * R::RB;  // dO
+    unsigned char* T2 = smem + 7 * R::RB;  // dS2
+    unsigned char* T1 = T2 + R::TB;        // dS
+    unsigned char* Ta = T2 + 2 * R::TB;    // Pa
+    const T* Qg = slice<T>(a.q, b, h);
+    const T* gQg = slice<T>(a.gq, b, h);
+    const T* Og = slice<T>(a.dO, b, h);
+    const float sc = a.scale;
+    const float sc2 = sc * LOG2E;
+    const int row0 = w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    const LaneOff<T, DP> lo(w.l16, w.g);
+
+    // Loads, in this order: K, gK, V, gV (needed first), the own rows, then Q, gQ, dO (needed by the col pass).
+    async_rows<T, DP>(Kr, slice<T>(a.k, b, h), a.k.sl, L, Lp, w.wave, R::NW, w.lane);
+    async_rows<T, DP>(gKr, slice<T>(a.gk, b, h), a.gk.sl, L, Lp, w.wave, R::NW, w.lane);
+    async_rows<T, DP>(Vr, slice<T>(a.v, b, h), a.v.sl, L, Lp, w.wave, R::NW, w.lane);
+    async_rows<T, DP>(gVr, slice<T>(a.gv, b, h), a.gv.sl, L, Lp, w.wave, R::NW, w.lane);
+    OwnFrag<T, DP> qf, gqf, df, of;
+    load_own<T, DP>(qf, Qg, a.q.sl, own, L, DP, w.g);
+    load_own<T, DP>(gqf, gQg, a.gq.sl, own, L, DP, w.g);
+    load_own<T, DP>(df, Og, a.dO.sl, own, L, DP, w.g);
+    load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
+    const float lraw = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)];  // unconditional load
+        const float lse2 = (own < L) ? lraw * LOG2E : 0.f;
+    async_rows<T, DP>(Qr, Qg, a.q.sl, L, Lp, w.wave, R::NW, w.lane);
+    async_rows<T, DP>(gQr, gQg, a.gq.sl, L, Lp, w.wave, R::NW, w.lane);
+    async_rows<T, DP>(Or, Og, a.dO.sl, L, Lp, w.wave, R::NW, w.lane);
+    // vmcnt(QLOADS) (expcnt and lgkmcnt not waited): every load older than this wave's QLOADS Q/gQ/dO blocks is done
+    __builtin_amdgcn_s_waitcnt(0x0f70 | R::QLOADS);
+    lds_barrier();
+
+    // ---- row pass: own = queries (as k_bb_res), plus the tile writes
+    if (active) {
+        const float dr = xsum4(frag_dot<T, DP>(df, of));
+        SeqB<T> m1b[NCH], dsb[NCH], pb[NCH], pab[NCH];
+        float e_acc = 0.f, t_acc = 0.f;
+        static_for<0, NCH>([&](auto cc) {
+            constexpr int C = decltype(cc)::value;
+            constexpr bool LAST = C == NCH - 1;
+            const int x0 = C * CH;
+            f32x4 p[2], dp[2], at[2], bm[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int r0 = x0 + 16 * hh;
+                mma_d_sw<T, DP>(p[hh], Kr, r0, qf, lo);
+                mma_d_sw<T, DP>(at[hh], Kr, r0, gqf, lo);
+                mma_d_sw<T, DP>(at[hh], gKr, r0, qf, lo);
+                mma_d_sw<T, DP>(dp[hh], Vr, r0, df, lo);
+                mma_d_sw<T, DP>(bm[hh], gVr, r0, df, lo);
+            }
+            f32x4 ds[2], pa[2], m1[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pv = row_p<LAST>(p[hh][r], sc2, lse2, x0 + 16 * hh + 4 * w.g + r, L);
+                    const float dsv = pv * (dp[hh][r] - dr);
+                    const float av = at[hh][r] * sc;
+                    p[hh][r] = pv;
+                    ds[hh][r] = dsv;
+                    pa[hh][r] = pv * av;
+                    m1[hh][r] = fmaf(dsv, av, pv * bm[hh][r]);
+                    e_acc += pa[hh][r];
+                    t_acc += m1[hh][r];
+                }
+            }
+            pb[C] = make_seqb<T>(p[0], p[1]);
+            dsb[C] = make_seqb<T>(ds[0], ds[1]);
+            pab[C] = make_seqb<T>(pa[0], pa[1]);
+            m1b[C] = make_seqb<T>(m1[0], m1[1]);
+        });
+        const float E = xsum4(e_acc);
+        const float Tm = xsum4(t_acc);
+        const bool real = own < L;  // padded query rows contribute nothing to hK, hV
+        f32x4 hq[LY::NT], hdo[LY::NT];
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) hq[t] = hdo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        static_for<0, NCH>([&](auto cc) {
+            constexpr int C = decltype(cc)::value;
+            const int x0 = C * CH;
+            float m1f[8], dsf[8], pf[8], paf[8], d2[8], pe[8];
+            unpack_seqb<T>(m1b[C], m1f);
+            unpack_seqb<T>(dsb[C], dsf);
+            unpack_seqb<T>(pb[C], pf);
+            unpack_seqb<T>(pab[C], paf);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                d2[e] = m1f[e] - E * dsf[e] - Tm * pf[e];
+                pe[e] = paf[e] - E * pf[e];
+            }
+            const SeqB<T> d2b = pack_seqb<T>(d2);
+            const SeqB<T> peb = pack_seqb<T>(pe);
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            const u32x4 w2 = real ? d2b.v : zero, w1 = real ? dsb[C].v : zero, wa = real ? peb.v : zero;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int key0 = x0 + 16 * hh + 4 * w.g;
+                tile_store8(T2, R::TP, own, key0, u32x2{w2[2 * hh], w2[2 * hh + 1]});
+                tile_store8(T1, R::TP, own, key0, u32x2{w1[2 * hh], w1[2 * hh + 1]});
+                tile_store8(Ta, R::TP, own, key0, u32x2{wa[2 * hh], wa[2 * hh + 1]});
+            }
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) {
+                hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(Kr, x0, t, lo), d2b);
+                hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, lo), dsb[C]);
+                hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(Vr, x0, t, lo), peb);
+                hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, lo), pb[C]);
+            }
+        });
+        if (real) {
+            const int64_t r = ((int64_t)bh * L + own) * DP;
+            store_rows<T, DP>(a.out0, r, hq, sc, DP, w.g);
+            store_rows<T, DP>(a.out3, r, hdo, 1.f, DP, w.g);
+        }
+    } else {
+        // rows of this wave are all past L: zero tile rows
+        const u32x2 z = {0u, 0u};
+#pragma unroll
+        for (int C = 0; C < NCH; ++C) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int key0 = C * CH + 16 * hh + 4 * w.g;
+                tile_store8(T2, R::TP, own, key0, z);
+                tile_store8(T1, R::TP, own, key0, z);
+                tile_store8(Ta, R::TP, own, key0, z);
+            }
+        }
+    }
+    async_wait();     // Q, gQ, dO
+    lds_barrier();  // tiles complete
+
+    // ---- col pass: own = keys; hK, hV from the tiles
+    if (!active) return;
+    f32x4 hk[LY::NT], hv[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    static_for<0, NCH>([&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+        const int x0 = C * CH;
+        const SeqB<T> b2 = tile_seqb<T>(T2, R::TP, x0, row0, w.l16, w.g);
+        const SeqB<T> b1 = tile_seqb<T>(T1, R::TP, x0, row0, w.l16, w.g);
+        const SeqB<T> ba = tile_seqb<T>(Ta, R::TP, x0, row0, w.l16, w.g);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, x0, t, lo), b2);
+            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, x0, t, lo), b1);
+            hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, x0, t, lo), ba);
         }
     });
     if (own < L) {

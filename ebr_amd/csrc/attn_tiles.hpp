@@ -114,6 +114,20 @@ __device__ __forceinline__ float xmax4(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations (lgkmcnt(0)), not for its global
+// loads, so loads issued before it stay in flight (``__syncthreads`` would wait for every memory operation).
+// Completion of global -> LDS loads is waited for explicitly with ``vm_wait`` before such a barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt(63), expcnt(7): not waited
+    __builtin_amdgcn_s_barrier();
+}
+
+// Wait until at most N of this wave's vector-memory operations are outstanding (N < 16).
+template <int N> __device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0f70 | N);
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // Own-side B fragments: lane (row = own, group g) holds d = c * CW + g * VEC + [0, VEC) for c < NC.
 // ---------------------------------------------------------------------------------------------------------------------
@@ -126,12 +140,15 @@ template <typename T, int DP>
 __device__ __forceinline__ void load_own(OwnFrag<T, DP>& f, const T* base, int64_t srow, int row, int L, int D,
                                          int g) {
     using LY = Lay<T, DP>;
-    const T* p = base + (int64_t)row * srow;
+    // Unconditional loads from a clamped (always valid) address, then a select: no branch, so the loads of several
+    // fragments stay in flight together.
+    const T* p = base + (int64_t)(row < L ? row : L - 1) * srow;
 #pragma unroll
     for (int c = 0; c < LY::NC; ++c) {
         const int d0 = c * LY::CW + g * LY::VEC;
-        u32x4 z = {0u, 0u, 0u, 0u};
-        f.v[c] = (row < L && d0 < D) ? *reinterpret_cast<const u32x4*>(p + d0) : z;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p + (d0 < D ? d0 : D - LY::VEC));
+        f.v[c] = (row < L && d0 < D) ? v : z;
     }
 }
 
@@ -291,10 +308,13 @@ template <typename T, int DP, int N> struct Stage {
             const int row = x0 + x;
             const int d0 = c * LY::VEC;
             const bool ok = it < TOTAL && row < L && d0 < D;
+            const int64_t rr = row < L ? row : L - 1;  // clamped: the load is unconditional (no branch)
+            const int dd = (it < TOTAL && d0 < D) ? d0 : D - LY::VEC;
 #pragma unroll
             for (int t = 0; t < N; ++t) {
-                u32x4 z = {0u, 0u, 0u, 0u};
-                r[t][i] = ok ? *reinterpret_cast<const u32x4*>(s.p[t] + (int64_t)row * s.srow[t] + d0) : z;
+                const u32x4 z = {0u, 0u, 0u, 0u};
+                const u32x4 v = *reinterpret_cast<const u32x4*>(s.p[t] + rr * s.srow[t] + dd);
+                r[t][i] = ok ? v : z;
             }
         }
     }
@@ -337,9 +357,14 @@ template <int NS> struct StatStage {
                                          int L, int tid) {
         const int x = x0 + tid;
         const bool ok = tid < CH && x < L;
-        r[0] = ok ? lse[row_base + x] : INFINITY;
+        const int64_t xc = row_base + (ok ? x : L - 1);  // clamped: unconditional loads, then selects
+        const float l0 = lse[xc];
+        r[0] = ok ? l0 : INFINITY;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) r[s + 1] = ok ? stats[s * bhl + row_base + x] : 0.f;
+        for (int s = 0; s < NS; ++s) {
+            const float v = stats[s * bhl + xc];
+            r[s + 1] = ok ? v : 0.f;
+        }
     }
     __device__ __forceinline__ void store(float* st, int tid) const {
         if (tid < CH) {

@@ -130,9 +130,9 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd(Args 
     const float sc = a.scale;
 
     for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
+        lds_barrier();
         stg.store(nat, tr, w.tid, w.nthr);
-        __syncthreads();
+        lds_barrier();
         if (x0 + CH < L) stg.load(src, x0 + CH, L, D, w.tid, w.nthr);
         if (!active) continue;
         f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -216,7 +216,8 @@ template <typename T, int DP, bool FUSED> struct BwdRow {
         load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, D, w.g);
         load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, D, w.g);
         load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * D, D, own, L, D, w.g);
-        lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
+        const float lraw = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)];  // unconditional load
+        lse = (own < L) ? lraw : 0.f;
         dr = xsum4(frag_dot<T, DP>(df, of));
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -370,7 +371,8 @@ template <typename T, int DP, bool FUSED> struct BbRow {
         load_own<T, DP>(gqf, slice<T>(a.gq, b, h), a.gq.sl, own, L, D, w.g);
         load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, D, w.g);
         load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * D, D, own, L, D, w.g);
-        lse = (own < L) ? a.lse[(int64_t)bh * L + own] : 0.f;
+        const float lraw = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)];  // unconditional load
+        lse = (own < L) ? lraw : 0.f;
         dr = xsum4(frag_dot<T, DP>(df, of));
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) X[t] = U[t] = Z[t] = Wv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -592,16 +594,16 @@ __device__ __forceinline__ void fused_two_pass(const Args& a, unsigned char* sme
     col.lds(smem, cn, ct);
 
     rst.load(rsrc, 0, L, D, w.tid, w.nthr);
-    __syncthreads();  // statistics defaults visible before the row pass publishes
+    lds_barrier();  // statistics defaults visible before the row pass publishes
     if constexpr (NSTAT == 1) {
         row.init(a, bh, 0, w, st);
     } else {
         row.init(a, bh, 0, w);
     }
     for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
+        lds_barrier();
         rst.store(rn, rt, w.tid, w.nthr);
-        __syncthreads();
+        lds_barrier();
         if (x0 + CH < L)
             rst.load(rsrc, x0 + CH, L, D, w.tid, w.nthr);
         else
@@ -615,9 +617,9 @@ __device__ __forceinline__ void fused_two_pass(const Args& a, unsigned char* sme
     }
     col.init(a, bh, 0, w);
     for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
+        lds_barrier();
         cst.store(cn, ct, w.tid, w.nthr);
-        __syncthreads();
+        lds_barrier();
         if (x0 + CH < L) cst.load(csrc, x0 + CH, L, D, w.tid, w.nthr);
         col.chunk(a, smem, st + x0, STAT_MAX, w);
     }
@@ -666,9 +668,9 @@ __device__ __forceinline__ void stream_row(const Args& a, unsigned char* smem) {
         row.init(a, bh, blk * (w.nthr >> 2), w, nullptr);
     }
     for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
+        lds_barrier();
         rst.store(rn, rt, w.tid, w.nthr);
-        __syncthreads();
+        lds_barrier();
         if (x0 + CH < L) rst.load(src, x0 + CH, L, D, w.tid, w.nthr);
         row.chunk(a, x0, smem, w);
     }
@@ -700,10 +702,10 @@ __device__ __forceinline__ void stream_col(const Args& a, unsigned char* smem) {
     sst.load(a.lse, a.stats, a.bhl, rb, 0, L, w.tid);
     col.init(a, bh, blk * (w.nthr >> 2), w);
     for (int x0 = 0; x0 < L; x0 += CH) {
-        __syncthreads();
+        lds_barrier();
         cst.store(cn, ct, w.tid, w.nthr);
         sst.store(stc, w.tid);
-        __syncthreads();
+        lds_barrier();
         if (x0 + CH < L) {
             cst.load(src, x0 + CH, L, D, w.tid, w.nthr);
             sst.load(a.lse, a.stats, a.bhl, rb, x0 + CH, L, w.tid);
@@ -899,7 +901,17 @@ template <typename T, int DP> struct BbLaunch {
             if (!resident_shape(a, DP, (int)sizeof(T), true)) {
                 hipLaunchKernelGGL((k_bb_fused<T, DP>), grid, block, 0, s, a);
             } else if constexpr (!ET<T>::F32) {
-                switch ((a.L + CH - 1) / CH) {
+                const int nch = (a.L + CH - 1) / CH;
+                if constexpr (DP <= 64) {
+                    if (nch <= 3) {  // tiles shared through LDS (k_bb_share): one wave per 16 rows of the padded L
+                        const dim3 blk(64 * 2 * nch);
+                        if (nch == 1) hipLaunchKernelGGL((k_bb_share<T, DP, 1>), grid, blk, 0, s, a);
+                        if (nch == 2) hipLaunchKernelGGL((k_bb_share<T, DP, 2>), grid, blk, 0, s, a);
+                        if (nch == 3) hipLaunchKernelGGL((k_bb_share<T, DP, 3>), grid, blk, 0, s, a);
+                        return launch_rc();
+                    }
+                }
+                switch (nch) {
                     case 1: hipLaunchKernelGGL((k_bb_res<T, DP, 1>), grid, block, 0, s, a); break;
                     case 2: hipLaunchKernelGGL((k_bb_res<T, DP, 2>), grid, block, 0, s, a); break;
                     case 3: hipLaunchKernelGGL((k_bb_res<T, DP, 3>), grid, block, 0, s, a); break;
