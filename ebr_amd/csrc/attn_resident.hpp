@@ -213,7 +213,10 @@ template <typename T, int DP, int NCH> struct BwdRes {
     static constexpr int SMEM = (SEP ? 4 : 2) * RB;
 };
 
-template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bwd_res(Args a) {
+// At most 102 VGPRs (5 waves per SIMD), so that as many workgroups share a CU as its LDS holds: at L = 81, three of
+// 6 waves and 50 KB each; the unconstrained build took 118 VGPRs and fit two.
+template <typename T, int DP, int NCH>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(DP <= 64 && NCH <= 3 ? 5 : 1, 8))) void k_bwd_res(Args a) {
     using LY = Lay<T, DP>;
     using R = BwdRes<T, DP, NCH>;
     constexpr int Lp = NCH * CH;
@@ -628,7 +631,6 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     load_own<T, DP>(df, Og, a.dO.sl, own, L, DP, w.g);
     load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
     const float lraw = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)];  // unconditional load
-        const float lse2 = (own < L) ? lraw * LOG2E : 0.f;
     async_rows<T, DP>(Qr, Qg, a.q.sl, L, Lp, w.wave, R::NW, w.lane);
     async_rows<T, DP>(gQr, gQg, a.gq.sl, L, Lp, w.wave, R::NW, w.lane);
     async_rows<T, DP>(Or, Og, a.dO.sl, L, Lp, w.wave, R::NW, w.lane);
@@ -636,10 +638,13 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     __builtin_amdgcn_s_waitcnt(0x0f70 | R::QLOADS);
     lds_barrier();
 
-    // ---- row pass: own = queries (as k_bb_res), plus the tile writes
+    // ---- row pass: own = queries (as k_bb_res), plus the tile writes. P, dS, PA and M1 stay in fp32 registers
+    // between the phases (the workgroup's LDS already limits the CU to one workgroup, so registers are not the
+    // occupancy limit); only MFMA operands and tiles are rounded to the input type.
     if (active) {
+        const float lse2 = (own < L) ? lraw * LOG2E : INFINITY;  // padded query rows: P = 0, so their tile rows are 0
         const float dr = xsum4(frag_dot<T, DP>(df, of));
-        SeqB<T> m1b[NCH], dsb[NCH], pb[NCH], pab[NCH];
+        float pf[NCH][8], dsf[NCH][8], paf[NCH][8], m1f[NCH][8];
         float e_acc = 0.f, t_acc = 0.f;
         static_for<0, NCH>([&](auto cc) {
             constexpr int C = decltype(cc)::value;
@@ -656,66 +661,57 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 mma_d_sw<T, DP>(dp[hh], Vr, r0, df, lo);
                 mma_d_sw<T, DP>(bm[hh], gVr, r0, df, lo);
             }
-            f32x4 ds[2], pa[2], m1[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
+                    const int e = 4 * hh + r;
                     const float pv = row_p<LAST>(p[hh][r], sc2, lse2, x0 + 16 * hh + 4 * w.g + r, L);
                     const float dsv = pv * (dp[hh][r] - dr);
                     const float av = at[hh][r] * sc;
-                    p[hh][r] = pv;
-                    ds[hh][r] = dsv;
-                    pa[hh][r] = pv * av;
-                    m1[hh][r] = fmaf(dsv, av, pv * bm[hh][r]);
-                    e_acc += pa[hh][r];
-                    t_acc += m1[hh][r];
+                    pf[C][e] = pv;
+                    dsf[C][e] = dsv;
+                    paf[C][e] = pv * av;
+                    m1f[C][e] = fmaf(dsv, av, pv * bm[hh][r]);
+                    e_acc += paf[C][e];
+                    t_acc += m1f[C][e];
                 }
             }
-            pb[C] = make_seqb<T>(p[0], p[1]);
-            dsb[C] = make_seqb<T>(ds[0], ds[1]);
-            pab[C] = make_seqb<T>(pa[0], pa[1]);
-            m1b[C] = make_seqb<T>(m1[0], m1[1]);
         });
         const float E = xsum4(e_acc);
         const float Tm = xsum4(t_acc);
-        const bool real = own < L;  // padded query rows contribute nothing to hK, hV
         f32x4 hq[LY::NT], hdo[LY::NT];
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) hq[t] = hdo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         static_for<0, NCH>([&](auto cc) {
             constexpr int C = decltype(cc)::value;
             const int x0 = C * CH;
-            float m1f[8], dsf[8], pf[8], paf[8], d2[8], pe[8];
-            unpack_seqb<T>(m1b[C], m1f);
-            unpack_seqb<T>(dsb[C], dsf);
-            unpack_seqb<T>(pb[C], pf);
-            unpack_seqb<T>(pab[C], paf);
+            float d2[8], pe[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                d2[e] = m1f[e] - E * dsf[e] - Tm * pf[e];
-                pe[e] = paf[e] - E * pf[e];
+                d2[e] = m1f[C][e] - E * dsf[C][e] - Tm * pf[C][e];
+                pe[e] = paf[C][e] - E * pf[C][e];
             }
             const SeqB<T> d2b = pack_seqb<T>(d2);
+            const SeqB<T> dsb = pack_seqb<T>(dsf[C]);
             const SeqB<T> peb = pack_seqb<T>(pe);
-            const u32x4 zero = {0u, 0u, 0u, 0u};
-            const u32x4 w2 = real ? d2b.v : zero, w1 = real ? dsb[C].v : zero, wa = real ? peb.v : zero;
+            const SeqB<T> pb = pack_seqb<T>(pf[C]);
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int key0 = x0 + 16 * hh + 4 * w.g;
-                tile_store8(T2, R::TP, own, key0, u32x2{w2[2 * hh], w2[2 * hh + 1]});
-                tile_store8(T1, R::TP, own, key0, u32x2{w1[2 * hh], w1[2 * hh + 1]});
-                tile_store8(Ta, R::TP, own, key0, u32x2{wa[2 * hh], wa[2 * hh + 1]});
+                tile_store8(T2, R::TP, own, key0, u32x2{d2b.v[2 * hh], d2b.v[2 * hh + 1]});
+                tile_store8(T1, R::TP, own, key0, u32x2{dsb.v[2 * hh], dsb.v[2 * hh + 1]});
+                tile_store8(Ta, R::TP, own, key0, u32x2{peb.v[2 * hh], peb.v[2 * hh + 1]});
             }
 #pragma unroll
             for (int t = 0; t < LY::NT; ++t) {
                 hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(Kr, x0, t, lo), d2b);
-                hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, lo), dsb[C]);
+                hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, lo), dsb);
                 hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(Vr, x0, t, lo), peb);
-                hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, lo), pb[C]);
+                hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, lo), pb);
             }
         });
-        if (real) {
+        if (own < L) {
             const int64_t r = ((int64_t)bh * L + own) * DP;
             store_rows<T, DP>(a.out0, r, hq, sc, DP, w.g);
             store_rows<T, DP>(a.out3, r, hdo, 1.f, DP, w.g);
