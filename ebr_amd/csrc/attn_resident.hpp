@@ -557,8 +557,22 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
 // [query][key] rows. The col pass then needs neither the scores nor any elementwise work: with A = Q, gQ, dO read
 // transposed from their natural rows and B = the tiles read transposed (lane = key, k-slots = queries),
 //   hK = s (dS2^T Q + dS^T gQ),  hV = Pa^T dO
-// are 3 GEMM units: 12 for the whole backward of the backward, the minimum. Q, gQ, dO have their own region and
-// are loaded while the row pass runs. One wave per 16 rows covers every tile row (padded rows are written as 0).
+// are 3 GEMM units: 12 for the whole backward of the backward, the minimum. One compute wave per 16 rows covers every
+// tile row (padded rows are written as 0).
+//
+// Persistent, with loader waves: the workgroup (one per CU: the regions fill its LDS) takes slices s, s + G, s + 2 G,
+// ... (G = gridDim.x). Besides the compute waves it has NWL loader waves, which hold the whole next slice in their
+// registers while the compute waves work on the current one, and write it into each region as soon as a barrier
+// frees it. They also reduce rowsum(dO o O) and scale lse, so the compute waves issue no global loads at all. The
+// loads go through registers (structured buffer loads) because an LDS transpose read right after an outstanding
+// global -> LDS load makes the compiler wait for that load. Per slice s with next slice n = s + G:
+//   compute waves                           loader waves
+//   row pass (s)                            load every input row of n into registers
+//   --- barrier A: tiles complete, K, gK, V, gV (s) no longer read
+//   store hQ, hdO (s); col pass (s)         write K, gK, V, gV (n)
+//   --- barrier B: tiles and Q, gQ, dO (s) no longer read
+//   store hK, hV (s)                        write Q, gQ, dO (n), rowsum(dO o O) (n), lse (n)
+//   --- barrier C: every region holds n
 // =====================================================================================================================
 
 template <typename T, int DP, int NCH> struct BbShare {
@@ -566,11 +580,65 @@ template <typename T, int DP, int NCH> struct BbShare {
     static constexpr int RB = LP * Sw<DP>::ROWB;  // one natural tensor region
     static constexpr int TP = LP * 2 + 32;        // tile row pitch (bytes), padded off the 256-byte bank period
     static constexpr int TB = LP * TP;            // one tile
-    static constexpr int SMEM = 7 * RB + 3 * TB;  // K, gK, V, gV | Q, gQ, dO | dS2, dS, Pa
-    static constexpr int NW = 2 * NCH;            // waves
-    // 1 KB buffer loads each wave issues for Q, gQ, dO (3 tensors x LP / RPI blocks over NW waves)
-    static constexpr int QLOADS = 3 * (LP / Sw<DP>::RPI) / NW;
+    static constexpr int NWC = 2 * NCH;           // compute waves (16 rows each)
+    static constexpr int NWL = 2;                 // loader waves
+    static constexpr int NB = LP / Sw<DP>::RPI;   // 1 KB blocks per tensor
+    static constexpr int NPER = NB / NWL;         // blocks per loader wave and tensor
+    static_assert(NPER * NWL == NB, "the loader waves split every tensor's 1 KB blocks evenly");
+    static_assert(NWL * 64 >= LP, "one loader lane per row for lse");
+    // K, gK, V, gV | Q, gQ, dO | dS2, dS, Pa | rowsum(dO o O), lse * log2 e
+    static constexpr int SMEM = 7 * RB + 3 * TB + 2 * LP * 4;
+    static constexpr int THREADS = 64 * (NWC + NWL);
 };
+
+// Structured buffer load (address = base + index * stride + offset; the stride, in bytes, sits in the descriptor).
+__device__ u32x4 ebr_struct_load_b128(__amdgpu_buffer_rsrc_t rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
+
+constexpr int64_t STRUCT_STRIDE_MAX = 16383;  // the descriptor's 14-bit stride field (bytes)
+
+// A loader wave's share of the 1 KB blocks of rows [0, LP) of one slice tensor: block q = wave + i * nw holds rows
+// q * RPI .. q * RPI + RPI - 1; lane l carries row x = q * RPI + l / NCK, chunk position l % NCK (global chunk
+// (l % NCK) ^ swz(x)), LDS offset 1024 q + 16 l. These lane values are the same for every tensor of the slice.
+template <int DP, int NPER> struct StageLanes {
+    int x[NPER], coff[NPER];
+    __device__ __forceinline__ StageLanes(int wave, int nw, int lane) {
+        using S = Sw<DP>;
+#pragma unroll
+        for (int i = 0; i < NPER; ++i) {
+            x[i] = (wave + i * nw) * S::RPI + lane / S::NCK;
+            coff[i] = 16 * ((lane % S::NCK) ^ S::swz(x[i]));
+        }
+    }
+};
+
+// Register staging of one tensor's share. fetch() issues the loads (row index clamped to L - 1, so every access is
+// inside the slice); put() writes them to a swizzled region, rows past L as 0.
+template <typename T, int DP, int NPER> struct RowStage {
+    u32x4 v[NPER];
+    __device__ __forceinline__ void fetch(const T* slice, int64_t srow, int L, const StageLanes<DP, NPER>& sl) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)slice, (short)(srow * (int64_t)sizeof(T)), 0x7fffffff, (int)BUF_RSRC_WORD3);
+#pragma unroll
+        for (int i = 0; i < NPER; ++i) v[i] = ebr_struct_load_b128(r, sl.x[i] < L ? sl.x[i] : L - 1, sl.coff[i], 0, 0);
+    }
+    __device__ __forceinline__ void put(unsigned char* region, int L, const StageLanes<DP, NPER>& sl, int wave, int nw,
+                                        int lane) const {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < NPER; ++i)
+            *reinterpret_cast<u32x4*>(region + (wave + i * nw) * 1024 + 16 * lane) = sl.x[i] < L ? v[i] : z;
+    }
+};
+
+template <typename T> __device__ __forceinline__ float dot8(u32x4 a, u32x4 b) {
+    using V8 = typename ET<T>::v8;
+    const V8 x = __builtin_bit_cast(V8, a), y = __builtin_bit_cast(V8, b);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += (float)x[e] * (float)y[e];
+    return s;
+}
 
 // 8-byte tile write: row ``row`` (query), keys key0 .. key0 + 3 (4 packed 16-bit values).
 __device__ __forceinline__ void tile_store8(unsigned char* tile, int pitch, int row, int key0, u32x2 v) {
@@ -591,15 +659,60 @@ __device__ __forceinline__ SeqB<T> tile_seqb(const unsigned char* tile, int pitc
     return b;
 }
 
+// The loader waves' registers: every input row of one slice.
+template <typename T, int DP, int NCH> struct BbLoader {
+    using R = BbShare<T, DP, NCH>;
+    using RS = RowStage<T, DP, R::NPER>;
+    StageLanes<DP, R::NPER> sl;
+    RS k, gk, v, gv, q, gq, dO, o;
+    float lse;
+    int lw, lane;
+    __device__ __forceinline__ BbLoader(int lw_, int lane_) : sl(lw_, R::NWL, lane_), lw(lw_), lane(lane_) {}
+    __device__ __forceinline__ void fetch(const Args& a, int s) {
+        const int L = a.L;
+        const int b = s / a.H, h = s - b * a.H;
+        k.fetch(slice<T>(a.k, b, h), a.k.sl, L, sl);
+        gk.fetch(slice<T>(a.gk, b, h), a.gk.sl, L, sl);
+        v.fetch(slice<T>(a.v, b, h), a.v.sl, L, sl);
+        gv.fetch(slice<T>(a.gv, b, h), a.gv.sl, L, sl);
+        q.fetch(slice<T>(a.q, b, h), a.q.sl, L, sl);
+        gq.fetch(slice<T>(a.gq, b, h), a.gq.sl, L, sl);
+        dO.fetch(slice<T>(a.dO, b, h), a.dO.sl, L, sl);
+        o.fetch(reinterpret_cast<const T*>(a.o) + (int64_t)s * L * DP, DP, L, sl);
+        const int t = lw * 64 + lane;
+        lse = a.lse[(int64_t)s * L + (t < L ? t : L - 1)];  // unconditional load
+    }
+    __device__ __forceinline__ void put_k4(unsigned char* smem, int L) const {
+        k.put(smem, L, sl, lw, R::NWL, lane);
+        gk.put(smem + R::RB, L, sl, lw, R::NWL, lane);
+        v.put(smem + 2 * R::RB, L, sl, lw, R::NWL, lane);
+        gv.put(smem + 3 * R::RB, L, sl, lw, R::NWL, lane);
+    }
+    __device__ __forceinline__ void put_rest(unsigned char* smem, float* dr, float* lse2, int L) const {
+        q.put(smem + 4 * R::RB, L, sl, lw, R::NWL, lane);
+        gq.put(smem + 5 * R::RB, L, sl, lw, R::NWL, lane);
+        dO.put(smem + 6 * R::RB, L, sl, lw, R::NWL, lane);
+        constexpr int NCK = Sw<DP>::NCK;
+#pragma unroll
+        for (int i = 0; i < R::NPER; ++i) {  // rowsum(dO o O): the row's NCK lanes hold its chunks of both
+            float d = dot8<T>(dO.v[i], o.v[i]);
+#pragma unroll
+            for (int m = 1; m < NCK; m <<= 1) d += __shfl_xor(d, m);
+            const int x = sl.x[i];
+            if (lane % NCK == 0) dr[x] = x < L ? d : 0.f;
+        }
+        const int t = lw * 64 + lane;
+        if (t < R::LP) lse2[t] = t < L ? lse * LOG2E : INFINITY;  // padded query rows: P = 0
+    }
+};
+
 template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bb_share(Args a) {
     using LY = Lay<T, DP>;
     using R = BbShare<T, DP, NCH>;
-    constexpr int Lp = R::LP;
     __shared__ __align__(1024) unsigned char smem[R::SMEM];
     const WaveIds w = wave_ids();
-    const int bh = blockIdx.x;
-    const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
+    const int nbh = a.B * a.H;
     unsigned char* Kr = smem;
     unsigned char* gKr = smem + R::RB;
     unsigned char* Vr = smem + 2 * R::RB;
@@ -610,150 +723,168 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     unsigned char* T2 = smem + 7 * R::RB;  // dS2
     unsigned char* T1 = T2 + R::TB;        // dS
     unsigned char* Ta = T2 + 2 * R::TB;    // Pa
-    const T* Qg = slice<T>(a.q, b, h);
-    const T* gQg = slice<T>(a.gq, b, h);
-    const T* Og = slice<T>(a.dO, b, h);
+    float* drl = reinterpret_cast<float*>(T2 + 3 * R::TB);
+    float* lsel = drl + R::LP;
+    int s = blockIdx.x;
+
+    if (w.wave >= R::NWC) {
+        // ---- loader waves
+        BbLoader<T, DP, NCH> ld(w.wave - R::NWC, w.lane);
+        ld.fetch(a, s);
+        ld.put_k4(smem, L);
+        ld.put_rest(smem, drl, lsel, L);
+        lds_barrier();
+        while (true) {
+            const int n = s + (int)gridDim.x;
+            const bool more = n < nbh;  // uniform over the workgroup
+            if (more) ld.fetch(a, n);
+            lds_barrier();  // A
+            if (more) ld.put_k4(smem, L);
+            lds_barrier();  // B
+            if (!more) break;
+            ld.put_rest(smem, drl, lsel, L);
+            lds_barrier();  // C
+            s = n;
+        }
+        return;
+    }
+
+    // ---- compute waves
     const float sc = a.scale;
     const float sc2 = sc * LOG2E;
     const int row0 = w.wave * 16;
     const int own = row0 + w.l16;
     const bool active = row0 < L;
     const LaneOff<T, DP> lo(w.l16, w.g);
+    lds_barrier();  // the first slice is in LDS
+    while (true) {
+        const int n = s + (int)gridDim.x;
+        const bool more = n < nbh;
 
-    // Loads, in this order: K, gK, V, gV (needed first), the own rows, then Q, gQ, dO (needed by the col pass).
-    async_rows<T, DP>(Kr, slice<T>(a.k, b, h), a.k.sl, L, Lp, w.wave, R::NW, w.lane);
-    async_rows<T, DP>(gKr, slice<T>(a.gk, b, h), a.gk.sl, L, Lp, w.wave, R::NW, w.lane);
-    async_rows<T, DP>(Vr, slice<T>(a.v, b, h), a.v.sl, L, Lp, w.wave, R::NW, w.lane);
-    async_rows<T, DP>(gVr, slice<T>(a.gv, b, h), a.gv.sl, L, Lp, w.wave, R::NW, w.lane);
-    OwnFrag<T, DP> qf, gqf, df, of;
-    load_own<T, DP>(qf, Qg, a.q.sl, own, L, DP, w.g);
-    load_own<T, DP>(gqf, gQg, a.gq.sl, own, L, DP, w.g);
-    load_own<T, DP>(df, Og, a.dO.sl, own, L, DP, w.g);
-    load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
-    const float lraw = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)];  // unconditional load
-    async_rows<T, DP>(Qr, Qg, a.q.sl, L, Lp, w.wave, R::NW, w.lane);
-    async_rows<T, DP>(gQr, gQg, a.gq.sl, L, Lp, w.wave, R::NW, w.lane);
-    async_rows<T, DP>(Or, Og, a.dO.sl, L, Lp, w.wave, R::NW, w.lane);
-    // vmcnt(QLOADS) (expcnt and lgkmcnt not waited): every load older than this wave's QLOADS Q/gQ/dO blocks is done
-    __builtin_amdgcn_s_waitcnt(0x0f70 | R::QLOADS);
-    lds_barrier();
-
-    // ---- row pass: own = queries (as k_bb_res), plus the tile writes. P, dS, PA and M1 stay in fp32 registers
-    // between the phases (the workgroup's LDS already limits the CU to one workgroup, so registers are not the
-    // occupancy limit); only MFMA operands and tiles are rounded to the input type.
-    if (active) {
-        const float lse2 = (own < L) ? lraw * LOG2E : INFINITY;  // padded query rows: P = 0, so their tile rows are 0
-        const float dr = xsum4(frag_dot<T, DP>(df, of));
-        float pf[NCH][8], dsf[NCH][8], paf[NCH][8], m1f[NCH][8];
-        float e_acc = 0.f, t_acc = 0.f;
-        static_for<0, NCH>([&](auto cc) {
-            constexpr int C = decltype(cc)::value;
-            constexpr bool LAST = C == NCH - 1;
-            const int x0 = C * CH;
-            f32x4 p[2], dp[2], at[2], bm[2];
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
-                const int r0 = x0 + 16 * hh;
-                mma_d_sw<T, DP>(p[hh], Kr, r0, qf, lo);
-                mma_d_sw<T, DP>(at[hh], Kr, r0, gqf, lo);
-                mma_d_sw<T, DP>(at[hh], gKr, r0, qf, lo);
-                mma_d_sw<T, DP>(dp[hh], Vr, r0, df, lo);
-                mma_d_sw<T, DP>(bm[hh], gVr, r0, df, lo);
-            }
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int e = 4 * hh + r;
-                    const float pv = row_p<LAST>(p[hh][r], sc2, lse2, x0 + 16 * hh + 4 * w.g + r, L);
-                    const float dsv = pv * (dp[hh][r] - dr);
-                    const float av = at[hh][r] * sc;
-                    pf[C][e] = pv;
-                    dsf[C][e] = dsv;
-                    paf[C][e] = pv * av;
-                    m1f[C][e] = fmaf(dsv, av, pv * bm[hh][r]);
-                    e_acc += paf[C][e];
-                    t_acc += m1f[C][e];
-                }
-            }
-        });
-        const float E = xsum4(e_acc);
-        const float Tm = xsum4(t_acc);
+        // ---- row pass: own = queries, plus the tile writes. P, dS, PA and M1 stay in fp32 registers between the
+        // phases; only MFMA operands and tiles are rounded to the input type.
         f32x4 hq[LY::NT], hdo[LY::NT];
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) hq[t] = hdo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        static_for<0, NCH>([&](auto cc) {
-            constexpr int C = decltype(cc)::value;
-            const int x0 = C * CH;
-            float d2[8], pe[8];
+        if (active) {
+            OwnFrag<T, DP> qf, gqf, df;
+            own_from_lds<T, DP>(qf, Qr, row0, lo);  // rows past L are 0 in the regions
+            own_from_lds<T, DP>(gqf, gQr, row0, lo);
+            own_from_lds<T, DP>(df, Or, row0, lo);
+            const float lse2 = lsel[own];
+            const float dr = drl[own];
+            float pf[NCH][8], dsf[NCH][8], paf[NCH][8], m1f[NCH][8];
+            float e_acc = 0.f, t_acc = 0.f;
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                constexpr bool LAST = C == NCH - 1;
+                const int x0 = C * CH;
+                f32x4 p[2], dp[2], at[2], bm[2];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                d2[e] = m1f[C][e] - E * dsf[C][e] - Tm * pf[C][e];
-                pe[e] = paf[C][e] - E * pf[C][e];
-            }
-            const SeqB<T> d2b = pack_seqb<T>(d2);
-            const SeqB<T> dsb = pack_seqb<T>(dsf[C]);
-            const SeqB<T> peb = pack_seqb<T>(pe);
-            const SeqB<T> pb = pack_seqb<T>(pf[C]);
+                for (int hh = 0; hh < 2; ++hh) {
+                    p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    const int r0 = x0 + 16 * hh;
+                    mma_d_sw<T, DP>(p[hh], Kr, r0, qf, lo);
+                    mma_d_sw<T, DP>(at[hh], Kr, r0, gqf, lo);
+                    mma_d_sw<T, DP>(at[hh], gKr, r0, qf, lo);
+                    mma_d_sw<T, DP>(dp[hh], Vr, r0, df, lo);
+                    mma_d_sw<T, DP>(bm[hh], gVr, r0, df, lo);
+                }
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int key0 = x0 + 16 * hh + 4 * w.g;
-                tile_store8(T2, R::TP, own, key0, u32x2{d2b.v[2 * hh], d2b.v[2 * hh + 1]});
-                tile_store8(T1, R::TP, own, key0, u32x2{dsb.v[2 * hh], dsb.v[2 * hh + 1]});
-                tile_store8(Ta, R::TP, own, key0, u32x2{peb.v[2 * hh], peb.v[2 * hh + 1]});
-            }
+                for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-            for (int t = 0; t < LY::NT; ++t) {
-                hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(Kr, x0, t, lo), d2b);
-                hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, lo), dsb);
-                hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(Vr, x0, t, lo), peb);
-                hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, lo), pb);
+                    for (int r = 0; r < 4; ++r) {
+                        const int e = 4 * hh + r;
+                        const float pv = row_p<LAST>(p[hh][r], sc2, lse2, x0 + 16 * hh + 4 * w.g + r, L);
+                        const float dsv = pv * (dp[hh][r] - dr);
+                        const float av = at[hh][r] * sc;
+                        pf[C][e] = pv;
+                        dsf[C][e] = dsv;
+                        paf[C][e] = pv * av;
+                        m1f[C][e] = fmaf(dsv, av, pv * bm[hh][r]);
+                        e_acc += paf[C][e];
+                        t_acc += m1f[C][e];
+                    }
+                }
+            });
+            const float E = xsum4(e_acc);
+            const float Tm = xsum4(t_acc);
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                const int x0 = C * CH;
+                float d2[8], pe[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    d2[e] = m1f[C][e] - E * dsf[C][e] - Tm * pf[C][e];
+                    pe[e] = paf[C][e] - E * pf[C][e];
+                }
+                const SeqB<T> d2b = pack_seqb<T>(d2);
+                const SeqB<T> dsb = pack_seqb<T>(dsf[C]);
+                const SeqB<T> peb = pack_seqb<T>(pe);
+                const SeqB<T> pb = pack_seqb<T>(pf[C]);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int key0 = x0 + 16 * hh + 4 * w.g;
+                    tile_store8(T2, R::TP, own, key0, u32x2{d2b.v[2 * hh], d2b.v[2 * hh + 1]});
+                    tile_store8(T1, R::TP, own, key0, u32x2{dsb.v[2 * hh], dsb.v[2 * hh + 1]});
+                    tile_store8(Ta, R::TP, own, key0, u32x2{peb.v[2 * hh], peb.v[2 * hh + 1]});
+                }
+#pragma unroll
+                for (int t = 0; t < LY::NT; ++t) {
+                    hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(Kr, x0, t, lo), d2b);
+                    hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, lo), dsb);
+                    hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(Vr, x0, t, lo), peb);
+                    hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, lo), pb);
+                }
+            });
+        } else {
+            // rows of this wave are all past L: zero tile rows
+            const u32x2 z = {0u, 0u};
+#pragma unroll
+            for (int C = 0; C < NCH; ++C) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int key0 = C * CH + 16 * hh + 4 * w.g;
+                    tile_store8(T2, R::TP, own, key0, z);
+                    tile_store8(T1, R::TP, own, key0, z);
+                    tile_store8(Ta, R::TP, own, key0, z);
+                }
             }
-        });
+        }
+        lds_barrier();  // A
         if (own < L) {
-            const int64_t r = ((int64_t)bh * L + own) * DP;
+            const int64_t r = ((int64_t)s * L + own) * DP;
             store_rows<T, DP>(a.out0, r, hq, sc, DP, w.g);
             store_rows<T, DP>(a.out3, r, hdo, 1.f, DP, w.g);
         }
-    } else {
-        // rows of this wave are all past L: zero tile rows
-        const u32x2 z = {0u, 0u};
-#pragma unroll
-        for (int C = 0; C < NCH; ++C) {
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int key0 = C * CH + 16 * hh + 4 * w.g;
-                tile_store8(T2, R::TP, own, key0, z);
-                tile_store8(T1, R::TP, own, key0, z);
-                tile_store8(Ta, R::TP, own, key0, z);
-            }
-        }
-    }
-    async_wait();     // Q, gQ, dO
-    lds_barrier();  // tiles complete
 
-    // ---- col pass: own = keys; hK, hV from the tiles
-    if (!active) return;
-    f32x4 hk[LY::NT], hv[LY::NT];
+        // ---- col pass: own = keys; hK, hV from the tiles
+        f32x4 hk[LY::NT], hv[LY::NT];
 #pragma unroll
-    for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    static_for<0, NCH>([&](auto cc) {
-        constexpr int C = decltype(cc)::value;
-        const int x0 = C * CH;
-        const SeqB<T> b2 = tile_seqb<T>(T2, R::TP, x0, row0, w.l16, w.g);
-        const SeqB<T> b1 = tile_seqb<T>(T1, R::TP, x0, row0, w.l16, w.g);
-        const SeqB<T> ba = tile_seqb<T>(Ta, R::TP, x0, row0, w.l16, w.g);
+        for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (active) {
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                const int x0 = C * CH;
+                const SeqB<T> b2 = tile_seqb<T>(T2, R::TP, x0, row0, w.l16, w.g);
+                const SeqB<T> b1 = tile_seqb<T>(T1, R::TP, x0, row0, w.l16, w.g);
+                const SeqB<T> ba = tile_seqb<T>(Ta, R::TP, x0, row0, w.l16, w.g);
 #pragma unroll
-        for (int t = 0; t < LY::NT; ++t) {
-            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, x0, t, lo), b2);
-            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, x0, t, lo), b1);
-            hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, x0, t, lo), ba);
+                for (int t = 0; t < LY::NT; ++t) {
+                    hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, x0, t, lo), b2);
+                    hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, x0, t, lo), b1);
+                    hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, x0, t, lo), ba);
+                }
+            });
         }
-    });
-    if (own < L) {
-        const int64_t r = ((int64_t)bh * L + own) * DP;
-        store_rows<T, DP>(a.out1, r, hk, sc, DP, w.g);
-        store_rows<T, DP>(a.out2, r, hv, 1.f, DP, w.g);
+        lds_barrier();  // B
+        if (own < L) {
+            const int64_t r = ((int64_t)s * L + own) * DP;
+            store_rows<T, DP>(a.out1, r, hk, sc, DP, w.g);
+            store_rows<T, DP>(a.out2, r, hv, 1.f, DP, w.g);
+        }
+        if (!more) break;
+        lds_barrier();  // C
+        s = n;
     }
 }

@@ -24,7 +24,10 @@
 #include <stdint.h>
 
 #include <cmath>
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "../../include/ebr_attn.h"
 #include "attn_tiles.hpp"
@@ -766,6 +769,14 @@ static bool resident_shape(const Args& a, int dp, int es, bool grads) {
     return ok;
 }
 
+// k_bb_share loads rows with structured buffer loads, whose descriptor holds the row stride in 14 bits.
+static bool struct_strides_fit(const Args& a) {
+    const Strided* t[7] = {&a.q, &a.k, &a.v, &a.dO, &a.gq, &a.gk, &a.gv};
+    for (const Strided* x : t)
+        if (x->sl * 2 > STRUCT_STRIDE_MAX) return false;
+    return true;
+}
+
 static int check_shape(int dtype, int B, int H, int L, int D) {
     if (dtype != EBR_DTYPE_F32 && dtype != EBR_DTYPE_BF16 && dtype != EBR_DTYPE_F16) return EBR_ERR_DTYPE;
     if (B < 1 || H < 1 || L < 1 || D < 1 || D > 128) return EBR_ERR_SHAPE;
@@ -801,6 +812,37 @@ static Strided mk(const void* p, const int64_t* s) {
 static int launch_rc() {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? EBR_OK : EBR_ERR_HIP_BASE + (int)e;
+}
+
+// Grid of a persistent kernel: as many workgroups as the current device holds at once (at most ``work``), cached per
+// kernel and device. One workgroup per work item when the runtime cannot tell (the kernels are correct at any grid).
+static int persistent_grid(const void* kernel, int threads, int64_t work) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, int> slots_of;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return (int)work;
+    }
+    int slots = 0;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        const auto it = slots_of.find({kernel, dev});
+        if (it != slots_of.end()) slots = it->second;
+    }
+    if (slots == 0) {
+        int ncu = 0, per = 0;
+        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || ncu < 1 ||
+            per < 1) {
+            (void)hipGetLastError();
+            return (int)work;
+        }
+        slots = ncu * per;
+        std::lock_guard<std::mutex> lk(mu);
+        slots_of[{kernel, dev}] = slots;
+    }
+    return (int)(work < slots ? work : slots);
 }
 
 template <template <typename, int> class F, typename... Rest>
@@ -903,11 +945,17 @@ template <typename T, int DP> struct BbLaunch {
             } else if constexpr (!ET<T>::F32) {
                 const int nch = (a.L + CH - 1) / CH;
                 if constexpr (DP <= 64) {
-                    if (nch <= 3) {  // tiles shared through LDS (k_bb_share): one wave per 16 rows of the padded L
-                        const dim3 blk(64 * 2 * nch);
-                        if (nch == 1) hipLaunchKernelGGL((k_bb_share<T, DP, 1>), grid, blk, 0, s, a);
-                        if (nch == 2) hipLaunchKernelGGL((k_bb_share<T, DP, 2>), grid, blk, 0, s, a);
-                        if (nch == 3) hipLaunchKernelGGL((k_bb_share<T, DP, 3>), grid, blk, 0, s, a);
+                    if (nch <= 3 && struct_strides_fit(a)) {  // tiles shared through LDS (k_bb_share)
+                        const int thr = nch == 1 ? BbShare<T, DP, 1>::THREADS
+                                        : nch == 2 ? BbShare<T, DP, 2>::THREADS
+                                                   : BbShare<T, DP, 3>::THREADS;
+                        const void* kfn = nch == 1   ? reinterpret_cast<const void*>(k_bb_share<T, DP, 1>)
+                                          : nch == 2 ? reinterpret_cast<const void*>(k_bb_share<T, DP, 2>)
+                                                     : reinterpret_cast<const void*>(k_bb_share<T, DP, 3>);
+                        const dim3 pg(persistent_grid(kfn, thr, bh)), blk(thr);
+                        if (nch == 1) hipLaunchKernelGGL((k_bb_share<T, DP, 1>), pg, blk, 0, s, a);
+                        if (nch == 2) hipLaunchKernelGGL((k_bb_share<T, DP, 2>), pg, blk, 0, s, a);
+                        if (nch == 3) hipLaunchKernelGGL((k_bb_share<T, DP, 3>), pg, blk, 0, s, a);
                         return launch_rc();
                     }
                 }
