@@ -344,6 +344,245 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(DP <= 64 &&
 }
 
 // =====================================================================================================================
+// Backward, persistent with a loader wave (16-bit inputs, D <= 64, L <= 96): two LDS buffers of K, V, Q, dO and lse.
+// The workgroup (one per CU) takes slices s, s + G, ... (G = gridDim.x); while its compute waves (one per 16 rows)
+// work on slice s in one buffer, the loader wave fills the other with slice s + G by global -> LDS loads. Compute
+// waves never have such a load outstanding, so their LDS transpose reads are never held back by one.
+// The row pass writes its P and dS tiles (rounded to the input type) as [query][key] rows; the col pass then is two
+// plain GEMMs from the tiles, dV = P^T dO and dK = s dS^T Q: 5 GEMM units for the backward, no recomputation.
+// The loader also scales lse and reduces rowsum(dO o O) of the next slice, so the compute waves issue no global loads.
+//   compute waves                     loader wave
+//   row pass (s): dQ, tiles           loads of slice n = s + G into the other buffer, its O rows into registers
+//   --- barrier X: tiles complete
+//   col pass (s): dK, dV              wait for the loads; lse (n) and rowsum(dO o O) (n) into the other buffer
+//   --- barrier Y: buffer of s and the tiles free, buffer of n complete
+// =====================================================================================================================
+
+// Dot product of two 8-element 16-bit vectors in fp32.
+template <typename T> __device__ __forceinline__ float dot8(u32x4 a, u32x4 b) {
+    using V8 = typename ET<T>::v8;
+    const V8 x = __builtin_bit_cast(V8, a), y = __builtin_bit_cast(V8, b);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += (float)x[e] * (float)y[e];
+    return s;
+}
+
+template <typename T, int DP, int NCH> struct BwdPipe {
+    static constexpr int LP = NCH * CH;
+    static constexpr int RB = LP * Sw<DP>::ROWB;  // one natural tensor region
+    static constexpr int TP = LP * 2 + 32;        // tile row pitch (bytes), padded off the 256-byte bank period
+    static constexpr int TB = LP * TP;            // one tile
+    static constexpr int NWC = 2 * NCH;           // compute waves
+    static constexpr int BUF = 4 * RB;            // K, V, Q, dO
+    // two buffers | P, dS tiles | lse * log2 e (two) | rowsum(dO o O) (two)
+    static constexpr int SMEM = 2 * BUF + 2 * TB + 4 * LP * 4;
+    static constexpr int THREADS = 64 * (NWC + 1);
+    static constexpr bool FITS = SMEM <= 160 * 1024;
+};
+
+// 8-byte tile write: row ``row`` (query), keys key0 .. key0 + 3 (4 packed 16-bit values).
+__device__ __forceinline__ void tile_store8(unsigned char* tile, int pitch, int row, int key0, u32x2 v) {
+    *reinterpret_cast<u32x2*>(tile + row * pitch + key0 * 2) = v;
+}
+
+// B operand of a col pass from a [query][key] tile: lane (key = kb + l16, group g), k-slot 4 h + k holds
+// tile[x0 + 16 h + 4 g + k][kb + l16].
+template <typename T>
+__device__ __forceinline__ SeqB<T> tile_seqb(const unsigned char* tile, int pitch, int x0, int kb, int l16, int g) {
+    const int k = l16 >> 2, j = l16 & 3;
+    const unsigned char* p = tile + (x0 + 4 * g + k) * pitch + (kb + 4 * j) * 2;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)p);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)(p + 16 * pitch));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    SeqB<T> b;
+    b.v = u32x4{l2[0], l2[1], h2[0], h2[1]};
+    return b;
+}
+
+// Zero the tile rows of a wave whose 16 rows are all past L.
+template <int NCH>
+__device__ __forceinline__ void zero_tile_rows(unsigned char* t0, unsigned char* t1, unsigned char* t2, int pitch,
+                                               int own, int g) {
+    const u32x2 z = {0u, 0u};
+#pragma unroll
+    for (int C = 0; C < NCH; ++C) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int key0 = C * CH + 16 * hh + 4 * g;
+            tile_store8(t0, pitch, own, key0, z);
+            tile_store8(t1, pitch, own, key0, z);
+            if (t2) tile_store8(t2, pitch, own, key0, z);
+        }
+    }
+}
+
+template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bwd_pipe(Args a) {
+    using LY = Lay<T, DP>;
+    using R = BwdPipe<T, DP, NCH>;
+    constexpr int Lp = R::LP;
+    __shared__ __align__(1024) unsigned char smem[R::SMEM];
+    const WaveIds w = wave_ids();
+    const int L = a.L;
+    const int nbh = a.B * a.H;
+    unsigned char* TPr = smem + 2 * R::BUF;  // P
+    unsigned char* TSr = TPr + R::TB;        // dS
+    float* lse_buf = reinterpret_cast<float*>(TPr + 2 * R::TB);  // [2][LP]
+    float* dr_buf = lse_buf + 2 * Lp;                              // [2][LP]
+    int s = blockIdx.x;
+
+    if (w.wave == R::NWC) {
+        // ---- loader wave: lane t handles rows t and t + 64 for lse and rowsum(dO o O)
+        constexpr int NCK = Sw<DP>::NCK;
+        const int t0 = w.lane, t1 = w.lane + 64;
+        float lv0 = 0.f, lv1 = 0.f;
+        u32x4 o0[NCK], o1[NCK];  // O rows t0, t1 (rows past L: row L - 1, finite; their rowsum is written as 0)
+        auto issue = [&](int sl, int bsel) {
+            const int b = sl / a.H, h = sl - b * a.H;
+            unsigned char* base = smem + bsel * R::BUF;
+            async_rows<T, DP>(base, slice<T>(a.k, b, h), a.k.sl, L, Lp, 0, 1, w.lane);
+            async_rows<T, DP>(base + R::RB, slice<T>(a.v, b, h), a.v.sl, L, Lp, 0, 1, w.lane);
+            async_rows<T, DP>(base + 2 * R::RB, slice<T>(a.q, b, h), a.q.sl, L, Lp, 0, 1, w.lane);
+            async_rows<T, DP>(base + 3 * R::RB, slice<T>(a.dO, b, h), a.dO.sl, L, Lp, 0, 1, w.lane);
+            lv0 = a.lse[(int64_t)sl * L + (t0 < L ? t0 : L - 1)];  // unconditional loads
+            lv1 = a.lse[(int64_t)sl * L + (t1 < L ? t1 : L - 1)];
+            const T* ob = reinterpret_cast<const T*>(a.o) + (int64_t)sl * L * DP;
+            const T* p0 = ob + (int64_t)(t0 < L ? t0 : L - 1) * DP;
+            const T* p1 = ob + (int64_t)(t1 < L ? t1 : L - 1) * DP;
+#pragma unroll
+            for (int c = 0; c < NCK; ++c) {
+                o0[c] = *reinterpret_cast<const u32x4*>(p0 + 8 * c);
+                o1[c] = *reinterpret_cast<const u32x4*>(p1 + 8 * c);
+            }
+        };
+        auto rowsum = [&](const unsigned char* dor, int t, const u32x4(&o)[NCK]) {
+            float d = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCK; ++c) d += dot8<T>(*reinterpret_cast<const u32x4*>(dor + Sw<DP>::off(t, c)), o[c]);
+            return t < L ? d : 0.f;
+        };
+        auto finish = [&](int bsel) {
+            async_wait();
+            float* l2 = lse_buf + bsel * Lp;
+            float* d2 = dr_buf + bsel * Lp;
+            const unsigned char* dor = smem + bsel * R::BUF + 3 * R::RB;
+            if (t0 < Lp) {
+                l2[t0] = t0 < L ? lv0 * LOG2E : INFINITY;  // padded query rows: P = 0
+                d2[t0] = rowsum(dor, t0, o0);
+            }
+            if (t1 < Lp) {
+                l2[t1] = t1 < L ? lv1 * LOG2E : INFINITY;
+                d2[t1] = rowsum(dor, t1, o1);
+            }
+        };
+        issue(s, 0);
+        finish(0);
+        lds_barrier();
+        for (int it = 0;; ++it) {
+            const int n = s + (int)gridDim.x;
+            const bool more = n < nbh;  // uniform over the workgroup
+            const int nb = (it & 1) ^ 1;
+            if (more) issue(n, nb);
+            lds_barrier();  // X
+            if (!more) break;
+            finish(nb);
+            lds_barrier();  // Y
+            s = n;
+        }
+        return;
+    }
+
+    // ---- compute waves
+    const float sc = a.scale;
+    const float sc2 = sc * LOG2E;
+    const int row0 = w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    const LaneOff<T, DP> lo(w.l16, w.g);
+    lds_barrier();  // the first slice is in buffer 0
+    for (int it = 0;; ++it) {
+        const int n = s + (int)gridDim.x;
+        const bool more = n < nbh;
+        const int bsel = it & 1;
+        unsigned char* Kr = smem + bsel * R::BUF;
+        unsigned char* Vr = Kr + R::RB;
+        unsigned char* Qr = Kr + 2 * R::RB;
+        unsigned char* Or = Kr + 3 * R::RB;  // dO
+        const float* l2 = lse_buf + bsel * Lp;
+
+        // ---- row pass: own = queries; dQ and the P, dS tiles
+        if (active) {
+            OwnFrag<T, DP> qf, df;
+            own_from_lds<T, DP>(qf, Qr, row0, lo);  // rows past L are 0 in the regions
+            own_from_lds<T, DP>(df, Or, row0, lo);
+            const float lse2 = l2[own];
+            const float dr = dr_buf[bsel * Lp + own];
+            f32x4 acc[LY::NT];
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                constexpr bool LAST = C == NCH - 1;
+                const int x0 = C * CH;
+                f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+                mma_d_sw<T, DP>(p0, Kr, x0, qf, lo);
+                mma_d_sw<T, DP>(p1, Kr, x0 + 16, qf, lo);
+                mma_d_sw<T, DP>(d0, Vr, x0, df, lo);
+                mma_d_sw<T, DP>(d1, Vr, x0 + 16, df, lo);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int x = x0 + 4 * w.g + r;
+                    p0[r] = row_p<LAST>(p0[r], sc2, lse2, x, L);  // lse = +inf on padded query rows -> P = 0
+                    p1[r] = row_p<LAST>(p1[r], sc2, lse2, x + 16, L);
+                    d0[r] = p0[r] * (d0[r] - dr);
+                    d1[r] = p1[r] * (d1[r] - dr);
+                }
+                const SeqB<T> pb = make_seqb<T>(p0, p1);
+                const SeqB<T> dsb = make_seqb<T>(d0, d1);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int key0 = x0 + 16 * hh + 4 * w.g;
+                    tile_store8(TPr, R::TP, own, key0, u32x2{pb.v[2 * hh], pb.v[2 * hh + 1]});
+                    tile_store8(TSr, R::TP, own, key0, u32x2{dsb.v[2 * hh], dsb.v[2 * hh + 1]});
+                }
+#pragma unroll
+                for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, x0, t, lo), dsb);
+            });
+            if (own < L) store_rows<T, DP>(a.out0, ((int64_t)s * L + own) * DP, acc, sc, DP, w.g);
+        } else {
+            zero_tile_rows<NCH>(TPr, TSr, nullptr, R::TP, own, w.g);
+        }
+        lds_barrier();  // X: tiles complete
+
+        // ---- col pass: own = keys; dV = P^T dO, dK = s dS^T Q from the tiles
+        if (active) {
+            f32x4 ak[LY::NT], av[LY::NT];
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                const int x0 = C * CH;
+                const SeqB<T> pb = tile_seqb<T>(TPr, R::TP, x0, row0, w.l16, w.g);
+                const SeqB<T> dsb = tile_seqb<T>(TSr, R::TP, x0, row0, w.l16, w.g);
+#pragma unroll
+                for (int t = 0; t < LY::NT; ++t) {
+                    av[t] = mma_seq<T>(av[t], seqa_tr<T, DP>(Or, x0, t, lo), pb);
+                    ak[t] = mma_seq<T>(ak[t], seqa_tr<T, DP>(Qr, x0, t, lo), dsb);
+                }
+            });
+            if (own < L) {
+                const int64_t r = ((int64_t)s * L + own) * DP;
+                store_rows<T, DP>(a.out1, r, ak, sc, DP, w.g);
+                store_rows<T, DP>(a.out2, r, av, 1.f, DP, w.g);
+            }
+        }
+        if (!more) break;
+        lds_barrier();  // Y: this buffer and the tiles free, the other buffer holds slice n
+        s = n;
+    }
+}
+
+// =====================================================================================================================
 // Backward of the backward: register-resident row pass, then the col pass.
 // Row pass, phase 1: the wave's 16 query rows x all keys of P, dS, M1 = dS A + P Bm and PA = P A, kept as packed
 // 16-bit MFMA operands, and the exact E = rowsum(PA), T = rowsum(M1). Phase 2: dS2 = M1 - E dS - T P and
@@ -631,33 +870,6 @@ template <typename T, int DP, int NPER> struct RowStage {
     }
 };
 
-template <typename T> __device__ __forceinline__ float dot8(u32x4 a, u32x4 b) {
-    using V8 = typename ET<T>::v8;
-    const V8 x = __builtin_bit_cast(V8, a), y = __builtin_bit_cast(V8, b);
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s += (float)x[e] * (float)y[e];
-    return s;
-}
-
-// 8-byte tile write: row ``row`` (query), keys key0 .. key0 + 3 (4 packed 16-bit values).
-__device__ __forceinline__ void tile_store8(unsigned char* tile, int pitch, int row, int key0, u32x2 v) {
-    *reinterpret_cast<u32x2*>(tile + row * pitch + key0 * 2) = v;
-}
-
-// B operand of the col pass from a [query][key] tile: lane (key = kb + l16, group g), k-slot 4 h + k holds
-// tile[x0 + 16 h + 4 g + k][kb + l16].
-template <typename T>
-__device__ __forceinline__ SeqB<T> tile_seqb(const unsigned char* tile, int pitch, int x0, int kb, int l16, int g) {
-    const int k = l16 >> 2, j = l16 & 3;
-    const unsigned char* p = tile + (x0 + 4 * g + k) * pitch + (kb + 4 * j) * 2;
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)p);
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)(p + 16 * pitch));
-    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-    SeqB<T> b;
-    b.v = u32x4{l2[0], l2[1], h2[0], h2[1]};
-    return b;
-}
 
 // The loader waves' registers: every input row of one slice.
 template <typename T, int DP, int NCH> struct BbLoader {
@@ -838,18 +1050,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 }
             });
         } else {
-            // rows of this wave are all past L: zero tile rows
-            const u32x2 z = {0u, 0u};
-#pragma unroll
-            for (int C = 0; C < NCH; ++C) {
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int key0 = C * CH + 16 * hh + 4 * w.g;
-                    tile_store8(T2, R::TP, own, key0, z);
-                    tile_store8(T1, R::TP, own, key0, z);
-                    tile_store8(Ta, R::TP, own, key0, z);
-                }
-            }
+            zero_tile_rows<NCH>(T2, T1, Ta, R::TP, own, w.g);
         }
         lds_barrier();  // A
         if (own < L) {

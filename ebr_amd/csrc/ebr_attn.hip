@@ -907,8 +907,25 @@ template <typename T, int DP> struct BwdLaunch {
             a.gq = a.gk = a.gv = a.dO;  // only q, k, v, dO are read
             if (resident_shape(a, DP, 2, true)) {
                 a.nblk = 1;
+                const int nch = (a.L + CH - 1) / CH;
+                if constexpr (DP <= 64) {
+                    if (nch <= 3) {  // persistent, double-buffered with a loader wave (k_bwd_pipe)
+                        static_assert(BwdPipe<T, DP, 3>::FITS, "two buffers fit the LDS");
+                        const int thr = nch == 1   ? BwdPipe<T, DP, 1>::THREADS
+                                        : nch == 2 ? BwdPipe<T, DP, 2>::THREADS
+                                                   : BwdPipe<T, DP, 3>::THREADS;
+                        const void* kfn = nch == 1   ? reinterpret_cast<const void*>(k_bwd_pipe<T, DP, 1>)
+                                          : nch == 2 ? reinterpret_cast<const void*>(k_bwd_pipe<T, DP, 2>)
+                                                     : reinterpret_cast<const void*>(k_bwd_pipe<T, DP, 3>);
+                        const dim3 pg(persistent_grid(kfn, thr, bh)), blk(thr);
+                        if (nch == 1) hipLaunchKernelGGL((k_bwd_pipe<T, DP, 1>), pg, blk, 0, s, a);
+                        if (nch == 2) hipLaunchKernelGGL((k_bwd_pipe<T, DP, 2>), pg, blk, 0, s, a);
+                        if (nch == 3) hipLaunchKernelGGL((k_bwd_pipe<T, DP, 3>), pg, blk, 0, s, a);
+                        return launch_rc();
+                    }
+                }
                 const dim3 grid((int)bh), block(fused_threads(a.L));
-                switch ((a.L + CH - 1) / CH) {
+                switch (nch) {
                     case 1: hipLaunchKernelGGL((k_bwd_res<T, DP, 1>), grid, block, 0, s, a); break;
                     case 2: hipLaunchKernelGGL((k_bwd_res<T, DP, 2>), grid, block, 0, s, a); break;
                     case 3: hipLaunchKernelGGL((k_bwd_res<T, DP, 3>), grid, block, 0, s, a); break;
