@@ -226,7 +226,9 @@ def bb_kernel_name(cfg: dict) -> str:
     if L > 128:
         return f"k_bb_row + k_bb_col <{DT_NAME[dt]}>"
     if dt != torch.float32 and D in (32, 64, 128):
-        return f"k_bb_res<{DT_NAME[dt]}, {D}, {(L + 31) // 32}>"
+        nch = (L + 31) // 32
+        kern = "k_bb_share" if D <= 64 and nch <= 3 else "k_bb_res"  # contiguous inputs: row strides fit
+        return f"{kern}<{DT_NAME[dt]}, {D}, {nch}>"
     return f"k_bb_fused<{DT_NAME[dt]}>"
 
 
