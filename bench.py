@@ -6,8 +6,9 @@ A step is one pass of the hot path over one batch: attn_fwd -> attn_bwd -> attn_
 Default workload: config 1 (Sudoku, bf16, B=768 H=8 L=81 D=64). Prints one JSON line.
 
 Timing: W untimed warm-up steps, then K steps bracketed by torch.cuda.synchronize(), timed with HIP events on the
-stream the kernels run on (torch's current stream). Steps rotate over several input sets (> the 256 MB MALL) so no
-step reads inputs the previous one left in the last-level cache. The dominant kernel (the backward of the backward)
+stream the kernels run on (torch's current stream). Steps rotate over enough input sets that their inputs alone
+exceed 512 MB, twice the 256 MB MALL, so a step's inputs have left the last-level cache since they were last read
+(cold-cache timing). The dominant kernel (the backward of the backward)
 is also timed alone through the C ABI with preallocated outputs, for the roofline entry.
 
 cpu_baseline: the CPU oracle (the build's restatement of the reference's eager path) timed on this host's cores on a
@@ -41,6 +42,15 @@ PHASES = ("fwd", "bwd", "bwd_bwd")
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+MALL_FLUSH_BYTES = 512 * 1024 * 1024  # twice the MI355X's 256 MB last-level (MALL) cache
+
+
+def cold_sets(cfg: dict) -> int:
+    """Input sets whose seven inputs together exceed MALL_FLUSH_BYTES (at least 3)."""
+    per = 7 * cfg["B"] * cfg["H"] * cfg["L"] * cfg["D"] * torch.tensor([], dtype=cfg["dtype"]).element_size()
+    return max(3, -(-MALL_FLUSH_BYTES // per))
 
 
 def make_sets(cfg: dict, dev: torch.device, nsets: int):
@@ -372,7 +382,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
-    ap.add_argument("--sets", type=int, default=3, help="input sets rotated across steps")
+    ap.add_argument("--sets", type=int, default=0,
+                    help="input sets rotated across steps (0: enough that their inputs exceed 512 MB)")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work (0 = skip)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -401,8 +412,9 @@ def main() -> int:
     scale = D**-0.5
     es = torch.tensor([], dtype=dt).element_size()
     dname = DT_NAME[dt]
-    log(f"workload {cfg['name']} B={B} H={H} L={L} D={D} {dname}; {args.sets} input sets")
-    sets = make_sets(cfg, dev, args.sets)
+    nsets = args.sets if args.sets > 0 else cold_sets(cfg)
+    log(f"workload {cfg['name']} B={B} H={H} L={L} D={D} {dname}; {nsets} input sets")
+    sets = make_sets(cfg, dev, nsets)
 
     sample = gpu_sample(cfg, sets, scale)
 

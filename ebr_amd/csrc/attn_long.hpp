@@ -1,0 +1,139 @@
+// Long-sequence kernels for 16-bit inputs (L > 128, D a supported width): a workgroup owns NWC * 16 rows of one
+// (b, h) slice and streams the other side through LDS in stages of LSTAGE rows.
+// Included inside namespace ebr by ebr_attn.hip, after attn_resident.hpp (uses its LDS layout and operand readers).
+//
+// Each workgroup has NWC compute waves (16 own rows each, kept in registers as MFMA B operands) and one loader wave.
+// The loader moves each stage global -> LDS (buffer_load ... lds; rows past L read as 0) into one of two stage
+// buffers while the compute waves work on the other, so compute waves never have such a load outstanding and their
+// LDS transpose reads are never held back by one. One barrier per stage hands a buffer over:
+//   loader:  issue(0); for i: { wait; barrier i; issue(i + 1) into the buffer stage i - 1 used }
+//   compute: for i: { barrier i; compute stage i }
+// Stage rows sit in the swizzled natural layout of the resident kernels; d-contractions read them as A operands,
+// seq-contractions read them transposed (ds_read_b64_tr_b16), so no transposed copy is ever written.
+
+constexpr int LSTAGE = 64;  // other-side rows per stage: two 32-row MFMA k-chunks
+constexpr float RESCALE_SLACK = 8.f;  // online softmax: headroom (log2 units) before the running maximum moves
+
+template <typename T, int DP, int NWC> struct LongCfg {
+    static constexpr int SB = LSTAGE * Sw<DP>::ROWB;  // one tensor's stage (bytes)
+    static constexpr int ROWS = 16 * NWC;             // own rows per workgroup
+    static constexpr int THREADS = 64 * (NWC + 1);
+};
+
+// Loader: rows [r0, r0 + LSTAGE) of one slice tensor into a stage region; rows past L read as 0.
+template <typename T, int DP>
+__device__ __forceinline__ void async_stage(unsigned char* region, const T* slice, int64_t srow, int L, int r0,
+                                            int lane) {
+    async_rows<T, DP>(region, slice + (int64_t)r0 * srow, srow, L - r0, LSTAGE, 0, 1, lane);
+}
+
+// The loader wave's loop over nst stages of ntens tensors each; ``issue(i, buf)`` starts stage i's loads into ``buf``
+// and ``after(i, buf)`` runs once they have landed (before the barrier that hands the buffer over).
+template <int STAGE_BYTES, class Issue, class After>
+__device__ __forceinline__ void loader_loop(unsigned char* smem, int nst, Issue&& issue, After&& after) {
+    issue(0, smem);
+    for (int i = 0; i < nst; ++i) {
+        async_wait();
+        after(i, smem + (i & 1) * STAGE_BYTES);
+        lds_barrier();
+        if (i + 1 < nst) issue(i + 1, smem + ((i + 1) & 1) * STAGE_BYTES);
+    }
+}
+
+// =====================================================================================================================
+// Forward: online softmax over the stages (reference point m in log2 units, running sum l, accumulator rescaled by
+// exp2(m_old - m_new) when m moves).
+// =====================================================================================================================
+
+template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 1)) void k_fwd_long(Args a) {
+    using LY = Lay<T, DP>;
+    using C = LongCfg<T, DP, NWC>;
+    constexpr int STB = 2 * C::SB;  // K, V
+    __shared__ __align__(1024) unsigned char smem[2 * STB];
+    const WaveIds w = wave_ids();
+    int bh, blk;
+    decode_block(a, bh, blk);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L;
+    const int nst = (L + LSTAGE - 1) / LSTAGE;
+
+    if (w.wave == NWC) {
+        const T* Kg = slice<T>(a.k, b, h);
+        const T* Vg = slice<T>(a.v, b, h);
+        loader_loop<STB>(
+            smem, nst,
+            [&](int i, unsigned char* buf) {
+                async_stage<T, DP>(buf, Kg, a.k.sl, L, i * LSTAGE, w.lane);
+                async_stage<T, DP>(buf + C::SB, Vg, a.v.sl, L, i * LSTAGE, w.lane);
+            },
+            [](int, unsigned char*) {});
+        return;
+    }
+
+    const int row0 = blk * C::ROWS + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;  // wave-uniform; inactive waves still take every barrier
+    OwnFrag<T, DP> qf;
+    load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, DP, w.g);
+    const LaneOff<T, DP> lo(w.l16, w.g);
+    const float sc2 = a.scale * LOG2E;  // scores in log2 units
+    f32x4 acc[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+    for (int i = 0; i < nst; ++i) {
+        lds_barrier();  // stage i in its buffer
+        if (!active) continue;
+        const unsigned char* Kr = smem + (i & 1) * STB;
+        const unsigned char* Vr = Kr + C::SB;
+        const int kb = i * LSTAGE;
+        f32x4 s[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            mma_d_sw<T, DP>(s[kt], Kr, 16 * kt, qf, lo);
+        }
+        if (kb + LSTAGE > L) {  // the last stage: keys past L
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (kb + 16 * kt + 4 * w.g + r >= L) s[kt][r] = -INFINITY;
+        }
+        float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+        for (int kt = 1; kt < 4; ++kt) mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
+        // Every stage holds at least one key below L, so the stage maximum is finite. The reference point m moves
+        // only when some row's maximum exceeds it by more than RESCALE_SLACK (wave vote): P stays <= 2^SLACK, and
+        // the accumulator is rescaled a few times per row instead of at every stage.
+        const float ms = xmax4(mx) * sc2;
+        if (__any(ms > m + RESCALE_SLACK)) {
+            const float mn = fmaxf(m, ms);
+            const float alpha = fast_exp2(m - mn);
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) acc[t] *= alpha;
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            f32x4 p0 = s[2 * c], p1 = s[2 * c + 1];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p0[r] = fast_exp2(fmaf(p0[r], sc2, -m));
+                p1[r] = fast_exp2(fmaf(p1[r], sc2, -m));
+                l += p0[r] + p1[r];
+            }
+            const SeqB<T> pb = make_seqb<T>(p0, p1);
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Vr, 32 * c, t, lo), pb);
+        }
+    }
+    if (!active) return;
+    l = xsum4(l);
+    if (own < L) {
+        const int64_t r = (int64_t)bh * L + own;
+        store_rows<T, DP>(a.out0, r * DP, acc, 1.f / l, DP, w.g);
+        if (w.g == 0) a.lse_out[r] = m * (1.f / LOG2E) + logf(l);
+    }
+}

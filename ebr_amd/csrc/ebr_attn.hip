@@ -649,6 +649,7 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_bb_fused(
 }
 
 #include "attn_resident.hpp"
+#include "attn_long.hpp"
 
 // Two-launch row kernel: own rows [blk * 16 W, (blk + 1) * 16 W) of one (b, h); statistics go to a.stats.
 template <typename T, int DP, class Row, int NROW, bool BB>
@@ -863,6 +864,25 @@ static int dispatch(int dtype, int D, Rest&&... rest) {
     return F<_Float16, 128>::run(rest...);
 }
 
+// The long-sequence kernels (16-bit inputs, L > 128): D a full chunk width, 32-bit buffer offsets per slice.
+constexpr int LONG_WAVES = 4;  // compute waves (x16 own rows) per workgroup of the long kernels
+static bool long_shape(const Args& a, int dp, bool grads) {
+    if (a.L <= STAT_MAX || a.D != dp) return false;
+    const int es = 2;
+    bool ok = strided_fits(a.q, a.L, a.D, es) && strided_fits(a.k, a.L, a.D, es) && strided_fits(a.v, a.L, a.D, es);
+    if (grads) {
+        ok = ok && strided_fits(a.dO, a.L, a.D, es) && strided_fits(a.gq, a.L, a.D, es) &&
+             strided_fits(a.gk, a.L, a.D, es) && strided_fits(a.gv, a.L, a.D, es);
+    }
+    return ok;
+}
+
+static void plan_long(Args& a, int64_t bh, int rows) {
+    a.nblk = (a.L + rows - 1) / rows;
+    a.xcd_remap = 1;
+    (void)bh;
+}
+
 static void plan_stream(Args& a, int64_t bh, int& grid, int& threads) {
     a.nblk = (a.L + 16 * STREAM_WAVES - 1) / (16 * STREAM_WAVES);
     a.xcd_remap = 1;
@@ -883,6 +903,15 @@ template <typename T, int DP> struct FwdLaunch {
                     case 3: hipLaunchKernelGGL((k_fwd_res<T, DP, 3>), grid, block, 0, s, a); break;
                     default: hipLaunchKernelGGL((k_fwd_res<T, DP, 4>), grid, block, 0, s, a); break;
                 }
+                return launch_rc();
+            }
+        }
+        if constexpr (!ET<T>::F32) {
+            if (long_shape(a, DP, false)) {  // streamed stages with a loader wave (k_fwd_long)
+                using C = LongCfg<T, DP, LONG_WAVES>;
+                plan_long(a, bh, C::ROWS);
+                hipLaunchKernelGGL((k_fwd_long<T, DP, LONG_WAVES>), dim3((int)(bh * a.nblk)), dim3(C::THREADS), 0, s,
+                                   a);
                 return launch_rc();
             }
         }
