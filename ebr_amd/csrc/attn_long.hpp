@@ -137,3 +137,187 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         if (w.g == 0) a.lse_out[r] = m * (1.f / LOG2E) + logf(l);
     }
 }
+
+// Loader helper: the statistics of a stage's LSTAGE rows [r0, r0 + LSTAGE) from fp32 [B, H, L] arrays, one row per
+// loader lane: lse * log2 e (+inf past L, so P = 0 there) and up to three further row statistics (0 past L).
+template <int NX> struct StageStats {
+    float lse, x[NX > 0 ? NX : 1];
+    __device__ __forceinline__ void load(const Args& a, int bh, int r0, int lane) {
+        const int L = a.L;
+        const int row = r0 + lane;
+        const int64_t i = (int64_t)bh * L + (row < L ? row : L - 1);  // unconditional loads
+        lse = a.lse[i];
+#pragma unroll
+        for (int k = 0; k < NX; ++k) x[k] = a.stats[k * a.bhl + i];
+    }
+    __device__ __forceinline__ void put(float* st, int r0, int L, int lane) const {
+        const bool in = r0 + lane < L;
+        st[lane] = in ? lse * LOG2E : INFINITY;
+#pragma unroll
+        for (int k = 0; k < NX; ++k) st[(k + 1) * LSTAGE + lane] = in ? x[k] : 0.f;
+    }
+};
+
+// =====================================================================================================================
+// Backward, row kernel: own = queries; dQ = s dS K over the K, V stages. Publishes Dr = rowsum(dO o O) of its rows
+// to a.stats for the col kernel.
+// =====================================================================================================================
+
+template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 1)) void k_bwd_long_row(Args a) {
+    using LY = Lay<T, DP>;
+    using C = LongCfg<T, DP, NWC>;
+    constexpr int STB = 2 * C::SB;  // K, V
+    __shared__ __align__(1024) unsigned char smem[2 * STB];
+    const WaveIds w = wave_ids();
+    int bh, blk;
+    decode_block(a, bh, blk);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L;
+    const int nst = (L + LSTAGE - 1) / LSTAGE;
+
+    if (w.wave == NWC) {
+        const T* Kg = slice<T>(a.k, b, h);
+        const T* Vg = slice<T>(a.v, b, h);
+        loader_loop<STB>(
+            smem, nst,
+            [&](int i, unsigned char* buf) {
+                async_stage<T, DP>(buf, Kg, a.k.sl, L, i * LSTAGE, w.lane);
+                async_stage<T, DP>(buf + C::SB, Vg, a.v.sl, L, i * LSTAGE, w.lane);
+            },
+            [](int, unsigned char*) {});
+        return;
+    }
+
+    const int row0 = blk * C::ROWS + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    OwnFrag<T, DP> qf, df, of;
+    load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, DP, w.g);
+    load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, DP, w.g);
+    load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
+    const float lraw = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)];  // unconditional load
+    const float lse2 = lraw * LOG2E;
+    const float dr = xsum4(frag_dot<T, DP>(df, of));
+    if (active && w.g == 0 && own < L) a.stats[(int64_t)bh * L + own] = dr;
+    const LaneOff<T, DP> lo(w.l16, w.g);
+    const float sc2 = a.scale * LOG2E;
+    f32x4 acc[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < nst; ++i) {
+        lds_barrier();  // stage i in its buffer
+        if (!active) continue;
+        const unsigned char* Kr = smem + (i & 1) * STB;
+        const unsigned char* Vr = Kr + C::SB;
+        const int kb = i * LSTAGE;
+        const bool last = kb + LSTAGE > L;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            f32x4 p[2], dp[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                p[hh] = dp[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                mma_d_sw<T, DP>(p[hh], Kr, 32 * c + 16 * hh, qf, lo);
+                mma_d_sw<T, DP>(dp[hh], Vr, 32 * c + 16 * hh, df, lo);
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
+                    if (last && kb + 32 * c + 16 * hh + 4 * w.g + r >= L) pv = 0.f;
+                    p[hh][r] = pv * (dp[hh][r] - dr);  // dS
+                }
+            const SeqB<T> dsb = make_seqb<T>(p[0], p[1]);
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, 32 * c, t, lo), dsb);
+        }
+    }
+    if (active && own < L) store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * DP, acc, a.scale, DP, w.g);
+}
+
+// =====================================================================================================================
+// Backward, col kernel: own = keys; dV = P^T dO and dK = s dS^T Q over the Q, dO stages, with the stages' lse and Dr.
+// =====================================================================================================================
+
+template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 1)) void k_bwd_long_col(Args a) {
+    using LY = Lay<T, DP>;
+    using C = LongCfg<T, DP, NWC>;
+    constexpr int STB = 2 * C::SB + 2 * LSTAGE * 4;  // Q, dO, [lse * log2 e | Dr]
+    __shared__ __align__(1024) unsigned char smem[2 * STB];
+    const WaveIds w = wave_ids();
+    int bh, blk;
+    decode_block(a, bh, blk);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L;
+    const int nst = (L + LSTAGE - 1) / LSTAGE;
+
+    if (w.wave == NWC) {
+        const T* Qg = slice<T>(a.q, b, h);
+        const T* Og = slice<T>(a.dO, b, h);
+        StageStats<1> stt;
+        loader_loop<STB>(
+            smem, nst,
+            [&](int i, unsigned char* buf) {
+                async_stage<T, DP>(buf, Qg, a.q.sl, L, i * LSTAGE, w.lane);
+                async_stage<T, DP>(buf + C::SB, Og, a.dO.sl, L, i * LSTAGE, w.lane);
+                stt.load(a, bh, i * LSTAGE, w.lane);
+            },
+            [&](int i, unsigned char* buf) {
+                stt.put(reinterpret_cast<float*>(buf + 2 * C::SB), i * LSTAGE, L, w.lane);
+            });
+        return;
+    }
+
+    const int row0 = blk * C::ROWS + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    OwnFrag<T, DP> kf, vf;
+    load_own<T, DP>(kf, slice<T>(a.k, b, h), a.k.sl, own, L, DP, w.g);
+    load_own<T, DP>(vf, slice<T>(a.v, b, h), a.v.sl, own, L, DP, w.g);
+    const LaneOff<T, DP> lo(w.l16, w.g);
+    const float sc2 = a.scale * LOG2E;
+    f32x4 ak[LY::NT], av[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < nst; ++i) {
+        lds_barrier();  // stage i in its buffer
+        if (!active) continue;
+        const unsigned char* Qr = smem + (i & 1) * STB;
+        const unsigned char* Or = Qr + C::SB;  // dO
+        const float* st = reinterpret_cast<const float*>(Qr + 2 * C::SB);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            f32x4 p[2], dp[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                p[hh] = dp[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                mma_d_sw<T, DP>(p[hh], Qr, 32 * c + 16 * hh, kf, lo);
+                mma_d_sw<T, DP>(dp[hh], Or, 32 * c + 16 * hh, vf, lo);
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int x = 32 * c + 16 * hh + 4 * w.g;
+                const f32x4 l2 = *reinterpret_cast<const f32x4*>(st + x);
+                const f32x4 d2 = *reinterpret_cast<const f32x4*>(st + LSTAGE + x);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    p[hh][r] = fast_exp2(fmaf(p[hh][r], sc2, -l2[r]));  // lse = +inf past L: P = 0
+                    dp[hh][r] = p[hh][r] * (dp[hh][r] - d2[r]);          // dS
+                }
+            }
+            const SeqB<T> pb = make_seqb<T>(p[0], p[1]);
+            const SeqB<T> dsb = make_seqb<T>(dp[0], dp[1]);
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) {
+                av[t] = mma_seq<T>(av[t], seqa_tr<T, DP>(Or, 32 * c, t, lo), pb);
+                ak[t] = mma_seq<T>(ak[t], seqa_tr<T, DP>(Qr, 32 * c, t, lo), dsb);
+            }
+        }
+    }
+    if (active && own < L) {
+        const int64_t r = ((int64_t)bh * L + own) * DP;
+        store_rows<T, DP>(a.out1, r, ak, a.scale, DP, w.g);
+        store_rows<T, DP>(a.out2, r, av, 1.f, DP, w.g);
+    }
+}
