@@ -321,3 +321,246 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         store_rows<T, DP>(a.out2, r, av, 1.f, DP, w.g);
     }
 }
+
+// =====================================================================================================================
+// Backward of the backward, row kernel: own = queries, over the K, gK, V, gV stages. E and T are complete only at the
+// end of the row, so the D-wide sums are kept apart (the reference's streaming form):
+//   X = sum (M1 K + dS gK), U = sum dS K, Z = sum P K, W = sum (PA V + P gV),
+//   hQ = s (X - E U - T Z),   hdO = W - E O   (with M1 = dS o A + P o Bm, PA = P o A).
+// Publishes Dr, E, T of its rows to a.stats ([3, B, H, L]) for the col kernel.
+// =====================================================================================================================
+
+template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 1)) void k_bb_long_row(Args a) {
+    using LY = Lay<T, DP>;
+    using C = LongCfg<T, DP, NWC>;
+    constexpr int STB = 4 * C::SB;  // K, gK, V, gV
+    __shared__ __align__(1024) unsigned char smem[2 * STB];
+    const WaveIds w = wave_ids();
+    int bh, blk;
+    decode_block(a, bh, blk);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L;
+    const int nst = (L + LSTAGE - 1) / LSTAGE;
+
+    if (w.wave == NWC) {
+        const T* Kg = slice<T>(a.k, b, h);
+        const T* gKg = slice<T>(a.gk, b, h);
+        const T* Vg = slice<T>(a.v, b, h);
+        const T* gVg = slice<T>(a.gv, b, h);
+        loader_loop<STB>(
+            smem, nst,
+            [&](int i, unsigned char* buf) {
+                const int r0 = i * LSTAGE;
+                async_stage<T, DP>(buf, Kg, a.k.sl, L, r0, w.lane);
+                async_stage<T, DP>(buf + C::SB, gKg, a.gk.sl, L, r0, w.lane);
+                async_stage<T, DP>(buf + 2 * C::SB, Vg, a.v.sl, L, r0, w.lane);
+                async_stage<T, DP>(buf + 3 * C::SB, gVg, a.gv.sl, L, r0, w.lane);
+            },
+            [](int, unsigned char*) {});
+        return;
+    }
+
+    const int row0 = blk * C::ROWS + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    OwnFrag<T, DP> qf, gqf, df;
+    float dr;
+    {
+        OwnFrag<T, DP> of;
+        load_own<T, DP>(qf, slice<T>(a.q, b, h), a.q.sl, own, L, DP, w.g);
+        load_own<T, DP>(gqf, slice<T>(a.gq, b, h), a.gq.sl, own, L, DP, w.g);
+        load_own<T, DP>(df, slice<T>(a.dO, b, h), a.dO.sl, own, L, DP, w.g);
+        load_own<T, DP>(of, reinterpret_cast<const T*>(a.o) + (int64_t)bh * L * DP, DP, own, L, DP, w.g);
+        dr = xsum4(frag_dot<T, DP>(df, of));
+    }
+    const float lse2 = a.lse[(int64_t)bh * L + (own < L ? own : L - 1)] * LOG2E;  // unconditional load
+    const LaneOff<T, DP> lo(w.l16, w.g);
+    const float sc = a.scale;
+    const float sc2 = sc * LOG2E;
+    f32x4 X[LY::NT], U[LY::NT], Z[LY::NT], W[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) X[t] = U[t] = Z[t] = W[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float e_acc = 0.f, t_acc = 0.f;
+    for (int i = 0; i < nst; ++i) {
+        lds_barrier();  // stage i in its buffer
+        if (!active) continue;
+        const unsigned char* Kr = smem + (i & 1) * STB;
+        const unsigned char* gKr = Kr + C::SB;
+        const unsigned char* Vr = Kr + 2 * C::SB;
+        const unsigned char* gVr = Kr + 3 * C::SB;
+        const int kb = i * LSTAGE;
+        const bool last = kb + LSTAGE > L;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            f32x4 p[2], at[2], dp[2], bm[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                p[hh] = at[hh] = dp[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int r0 = 32 * c + 16 * hh;
+                mma_d_sw<T, DP>(p[hh], Kr, r0, qf, lo);
+                mma_d_sw<T, DP>(at[hh], Kr, r0, gqf, lo);
+                mma_d_sw<T, DP>(at[hh], gKr, r0, qf, lo);
+                mma_d_sw<T, DP>(dp[hh], Vr, r0, df, lo);
+                mma_d_sw<T, DP>(bm[hh], gVr, r0, df, lo);
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
+                    if (last && kb + 32 * c + 16 * hh + 4 * w.g + r >= L) pv = 0.f;
+                    const float dsv = pv * (dp[hh][r] - dr);
+                    const float av = at[hh][r] * sc;
+                    const float pa = pv * av;
+                    const float m1 = fmaf(dsv, av, pv * bm[hh][r]);
+                    e_acc += pa;
+                    t_acc += m1;
+                    p[hh][r] = pv;
+                    dp[hh][r] = dsv;
+                    at[hh][r] = pa;
+                    bm[hh][r] = m1;
+                }
+            const SeqB<T> pb = make_seqb<T>(p[0], p[1]);
+            const SeqB<T> dsb = make_seqb<T>(dp[0], dp[1]);
+            const SeqB<T> pab = make_seqb<T>(at[0], at[1]);
+            const SeqB<T> m1b = make_seqb<T>(bm[0], bm[1]);
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) {
+                const SeqA<T> kt = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
+                X[t] = mma_seq<T>(X[t], kt, m1b);
+                X[t] = mma_seq<T>(X[t], seqa_tr<T, DP>(gKr, 32 * c, t, lo), dsb);
+                U[t] = mma_seq<T>(U[t], kt, dsb);
+                Z[t] = mma_seq<T>(Z[t], kt, pb);
+                W[t] = mma_seq<T>(W[t], seqa_tr<T, DP>(Vr, 32 * c, t, lo), pab);
+                W[t] = mma_seq<T>(W[t], seqa_tr<T, DP>(gVr, 32 * c, t, lo), pb);
+            }
+        }
+    }
+    if (!active) return;
+    const float E = xsum4(e_acc);
+    const float Tm = xsum4(t_acc);
+    if (own < L) {
+        const int64_t r = (int64_t)bh * L + own;
+        if (w.g == 0) {
+            a.stats[r] = dr;
+            a.stats[a.bhl + r] = E;
+            a.stats[2 * a.bhl + r] = Tm;
+        }
+        const T* orow = reinterpret_cast<const T*>(a.o) + r * DP;
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            X[t] = X[t] - E * U[t] - Tm * Z[t];
+            W[t] = W[t] - E * load4<T>(orow + 16 * t + 4 * w.g);  // O in the accumulator's lane layout
+        }
+        store_rows<T, DP>(a.out0, r * DP, X, sc, DP, w.g);
+        store_rows<T, DP>(a.out3, r * DP, W, 1.f, DP, w.g);
+    }
+}
+
+// =====================================================================================================================
+// Backward of the backward, col kernel: own = keys, over the Q, gQ, dO stages with the stages' lse, Dr, E, T:
+//   dS2 = dS o A + P o Bm - E dS - T P,  Pa = P o A - E P,  hK = s (dS2^T Q + dS^T gQ),  hV = Pa^T dO.
+// =====================================================================================================================
+
+template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 1)) void k_bb_long_col(Args a) {
+    using LY = Lay<T, DP>;
+    using C = LongCfg<T, DP, NWC>;
+    constexpr int STB = 3 * C::SB + 4 * LSTAGE * 4;  // Q, gQ, dO, [lse * log2 e | Dr | E | T]
+    __shared__ __align__(1024) unsigned char smem[2 * STB];
+    const WaveIds w = wave_ids();
+    int bh, blk;
+    decode_block(a, bh, blk);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int L = a.L;
+    const int nst = (L + LSTAGE - 1) / LSTAGE;
+
+    if (w.wave == NWC) {
+        const T* Qg = slice<T>(a.q, b, h);
+        const T* gQg = slice<T>(a.gq, b, h);
+        const T* Og = slice<T>(a.dO, b, h);
+        StageStats<3> stt;
+        loader_loop<STB>(
+            smem, nst,
+            [&](int i, unsigned char* buf) {
+                const int r0 = i * LSTAGE;
+                async_stage<T, DP>(buf, Qg, a.q.sl, L, r0, w.lane);
+                async_stage<T, DP>(buf + C::SB, gQg, a.gq.sl, L, r0, w.lane);
+                async_stage<T, DP>(buf + 2 * C::SB, Og, a.dO.sl, L, r0, w.lane);
+                stt.load(a, bh, r0, w.lane);
+            },
+            [&](int i, unsigned char* buf) {
+                stt.put(reinterpret_cast<float*>(buf + 3 * C::SB), i * LSTAGE, L, w.lane);
+            });
+        return;
+    }
+
+    const int row0 = blk * C::ROWS + w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;
+    OwnFrag<T, DP> kf, gkf, vf, gvf;
+    load_own<T, DP>(kf, slice<T>(a.k, b, h), a.k.sl, own, L, DP, w.g);
+    load_own<T, DP>(gkf, slice<T>(a.gk, b, h), a.gk.sl, own, L, DP, w.g);
+    load_own<T, DP>(vf, slice<T>(a.v, b, h), a.v.sl, own, L, DP, w.g);
+    load_own<T, DP>(gvf, slice<T>(a.gv, b, h), a.gv.sl, own, L, DP, w.g);
+    const LaneOff<T, DP> lo(w.l16, w.g);
+    const float sc = a.scale;
+    const float sc2 = sc * LOG2E;
+    f32x4 hk[LY::NT], hv[LY::NT];
+#pragma unroll
+    for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < nst; ++i) {
+        lds_barrier();  // stage i in its buffer
+        if (!active) continue;
+        const unsigned char* Qr = smem + (i & 1) * STB;
+        const unsigned char* gQr = Qr + C::SB;
+        const unsigned char* Or = Qr + 2 * C::SB;  // dO
+        const float* st = reinterpret_cast<const float*>(Qr + 3 * C::SB);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            f32x4 p[2], at[2], dp[2], bm[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                p[hh] = at[hh] = dp[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int x0 = 32 * c + 16 * hh;
+                mma_d_sw<T, DP>(p[hh], Qr, x0, kf, lo);
+                mma_d_sw<T, DP>(at[hh], gQr, x0, kf, lo);
+                mma_d_sw<T, DP>(at[hh], Qr, x0, gkf, lo);
+                mma_d_sw<T, DP>(dp[hh], Or, x0, vf, lo);
+                mma_d_sw<T, DP>(bm[hh], Or, x0, gvf, lo);
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int x = 32 * c + 16 * hh + 4 * w.g;
+                const f32x4 l2 = *reinterpret_cast<const f32x4*>(st + x);
+                const f32x4 d2 = *reinterpret_cast<const f32x4*>(st + LSTAGE + x);
+                const f32x4 e2 = *reinterpret_cast<const f32x4*>(st + 2 * LSTAGE + x);
+                const f32x4 t2 = *reinterpret_cast<const f32x4*>(st + 3 * LSTAGE + x);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pv = fast_exp2(fmaf(p[hh][r], sc2, -l2[r]));  // lse = +inf past L: P = 0
+                    const float dsv = pv * (dp[hh][r] - d2[r]);
+                    const float av = at[hh][r] * sc;
+                    const float pa = pv * av;
+                    const float m1 = fmaf(dsv, av, pv * bm[hh][r]);
+                    p[hh][r] = m1 - e2[r] * dsv - t2[r] * pv;  // dS2
+                    dp[hh][r] = dsv;
+                    at[hh][r] = pa - e2[r] * pv;  // Pa
+                }
+            }
+            const SeqB<T> d2b = make_seqb<T>(p[0], p[1]);
+            const SeqB<T> dsb = make_seqb<T>(dp[0], dp[1]);
+            const SeqB<T> peb = make_seqb<T>(at[0], at[1]);
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) {
+                hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, 32 * c, t, lo), d2b);
+                hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, 32 * c, t, lo), dsb);
+                hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, 32 * c, t, lo), peb);
+            }
+        }
+    }
+    if (active && own < L) {
+        const int64_t r = ((int64_t)bh * L + own) * DP;
+        store_rows<T, DP>(a.out1, r, hk, sc, DP, w.g);
+        store_rows<T, DP>(a.out2, r, hv, 1.f, DP, w.g);
+    }
+}

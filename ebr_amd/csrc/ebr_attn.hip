@@ -1026,6 +1026,18 @@ template <typename T, int DP> struct BbLaunch {
             }
             return launch_rc();
         }
+        if constexpr (!ET<T>::F32 && DP <= 64) {
+            if (long_shape(a, DP, true)) {  // streamed stages with a loader wave (k_bb_long_row, k_bb_long_col)
+                using C = LongCfg<T, DP, LONG_WAVES>;
+                plan_long(a, bh, C::ROWS);
+                const dim3 grid((int)(bh * a.nblk)), block(C::THREADS);
+                hipLaunchKernelGGL((k_bb_long_row<T, DP, LONG_WAVES>), grid, block, 0, s, a);
+                const int rc = launch_rc();
+                if (rc) return rc;
+                hipLaunchKernelGGL((k_bb_long_col<T, DP, LONG_WAVES>), grid, block, 0, s, a);
+                return launch_rc();
+            }
+        }
         int grid, threads;
         plan_stream(a, bh, grid, threads);
         hipLaunchKernelGGL((k_bb_row<T, DP>), dim3(grid), dim3(threads), 0, s, a);
