@@ -330,17 +330,19 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
 // Publishes Dr, E, T of its rows to a.stats ([3, B, H, L]) for the col kernel.
 // =====================================================================================================================
 
-template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 1)) void k_bb_long_row(Args a) {
+template <typename T, int DP, int NWC, int STG>
+__global__ __launch_bounds__(64 * (NWC + 1)) void k_bb_long_row(Args a) {
     using LY = Lay<T, DP>;
     using C = LongCfg<T, DP, NWC>;
-    constexpr int STB = 4 * C::SB;  // K, gK, V, gV
+    constexpr int SB = STG * Sw<DP>::ROWB;  // one tensor's stage
+    constexpr int STB = 4 * SB;              // K, gK, V, gV
     __shared__ __align__(1024) unsigned char smem[2 * STB];
     const WaveIds w = wave_ids();
     int bh, blk;
     decode_block(a, bh, blk);
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
-    const int nst = (L + LSTAGE - 1) / LSTAGE;
+    const int nst = (L + STG - 1) / STG;
 
     if (w.wave == NWC) {
         const T* Kg = slice<T>(a.k, b, h);
@@ -350,11 +352,11 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         loader_loop<STB>(
             smem, nst,
             [&](int i, unsigned char* buf) {
-                const int r0 = i * LSTAGE;
-                async_stage<T, DP>(buf, Kg, a.k.sl, L, r0, w.lane);
-                async_stage<T, DP>(buf + C::SB, gKg, a.gk.sl, L, r0, w.lane);
-                async_stage<T, DP>(buf + 2 * C::SB, Vg, a.v.sl, L, r0, w.lane);
-                async_stage<T, DP>(buf + 3 * C::SB, gVg, a.gv.sl, L, r0, w.lane);
+                const int r0 = i * STG;
+                async_rows<T, DP>(buf, Kg + (int64_t)r0 * a.k.sl, a.k.sl, L - r0, STG, 0, 1, w.lane);
+                async_rows<T, DP>(buf + SB, gKg + (int64_t)r0 * a.gk.sl, a.gk.sl, L - r0, STG, 0, 1, w.lane);
+                async_rows<T, DP>(buf + 2 * SB, Vg + (int64_t)r0 * a.v.sl, a.v.sl, L - r0, STG, 0, 1, w.lane);
+                async_rows<T, DP>(buf + 3 * SB, gVg + (int64_t)r0 * a.gv.sl, a.gv.sl, L - r0, STG, 0, 1, w.lane);
             },
             [](int, unsigned char*) {});
         return;
@@ -385,13 +387,13 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         lds_barrier();  // stage i in its buffer
         if (!active) continue;
         const unsigned char* Kr = smem + (i & 1) * STB;
-        const unsigned char* gKr = Kr + C::SB;
-        const unsigned char* Vr = Kr + 2 * C::SB;
-        const unsigned char* gVr = Kr + 3 * C::SB;
-        const int kb = i * LSTAGE;
-        const bool last = kb + LSTAGE > L;
+        const unsigned char* gKr = Kr + SB;
+        const unsigned char* Vr = Kr + 2 * SB;
+        const unsigned char* gVr = Kr + 3 * SB;
+        const int kb = i * STG;
+        const bool last = kb + STG > L;
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
+        for (int c = 0; c < STG / CH; ++c) {
             f32x4 p[2], at[2], dp[2], bm[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {

@@ -865,7 +865,8 @@ static int dispatch(int dtype, int D, Rest&&... rest) {
 }
 
 // The long-sequence kernels (16-bit inputs, L > 128): D a full chunk width, 32-bit buffer offsets per slice.
-constexpr int LONG_WAVES = 4;  // compute waves (x16 own rows) per workgroup of the long kernels
+constexpr int LONG_WAVES = 4;     // compute waves (x16 own rows) per workgroup of the long kernels
+constexpr int BB_ROW_STAGE = 64;  // k_bb_long_row's stage depth (32 rows with three workgroups per CU was slower)
 static bool long_shape(const Args& a, int dp, bool grads) {
     if (a.L <= STAT_MAX || a.D != dp) return false;
     const int es = 2;
@@ -1031,7 +1032,7 @@ template <typename T, int DP> struct BbLaunch {
                 using C = LongCfg<T, DP, LONG_WAVES>;
                 plan_long(a, bh, C::ROWS);
                 const dim3 grid((int)(bh * a.nblk)), block(C::THREADS);
-                hipLaunchKernelGGL((k_bb_long_row<T, DP, LONG_WAVES>), grid, block, 0, s, a);
+                hipLaunchKernelGGL((k_bb_long_row<T, DP, LONG_WAVES, BB_ROW_STAGE>), grid, block, 0, s, a);
                 const int rc = launch_rc();
                 if (rc) return rc;
                 hipLaunchKernelGGL((k_bb_long_col<T, DP, LONG_WAVES>), grid, block, 0, s, a);
