@@ -234,7 +234,9 @@ def bb_kernel_name(cfg: dict) -> str:
     """The kernel(s) ebr_attn_bwd_bwd dispatches for this workload (mirrors BbLaunch::run in ebr_attn.hip)."""
     L, D, dt = cfg["L"], cfg["D"], cfg["dtype"]
     if L > 128:
-        return f"k_bb_row + k_bb_col <{DT_NAME[dt]}>"
+        if dt != torch.float32 and D in (32, 64):
+            return f"k_bb_long_row<{DT_NAME[dt]}, {D}, 4, 64> + k_bb_long_col<{DT_NAME[dt]}, {D}, 4>"
+        return f"k_bb_row<{DT_NAME[dt]}, {D}> + k_bb_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32
         kern = "k_bb_share" if D <= 64 and nch <= 3 else "k_bb_res"  # contiguous inputs: row strides fit
@@ -252,10 +254,13 @@ def measured_traffic(config: int, kname: str):
             rec = json.load(f)
     except (OSError, ValueError):
         return None, None
-    k = rec.get("kernels", {}).get(kname)
-    if not k:
-        return None, None
-    return round(k["fetch_bytes"] + k["write_bytes"]), os.path.relpath(path, ROOT)
+    total = 0.0
+    for part in kname.split(" + "):  # a two-launch phase: the sum of its kernels' traffic
+        k = rec.get("kernels", {}).get(part)
+        if not k:
+            return None, None
+        total += k["fetch_bytes"] + k["write_bytes"]
+    return round(total), os.path.relpath(path, ROOT)
 
 
 def pmc_target(cfg: dict, reps: int = 3) -> None:
