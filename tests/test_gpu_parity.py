@@ -168,10 +168,11 @@ def test_config4_shape_bf16(cuda):
 # ---------------------------------------------------------------------------------------------------------------------
 
 
-def test_strided_views(cuda):
+@pytest.mark.parametrize("L", [81, 200])
+def test_strided_views(cuda, L):
     """q, k, v as transposed views of one [B, L, 3, H, D] projection (non-contiguous B/H/L strides)."""
-    B, H, L, D = 3, 4, 81, 64
-    _say("strided qkv views")
+    B, H, D = 3, 4, 64
+    _say(f"strided qkv views L={L}")
     g = torch.Generator().manual_seed(7)
     qkv = (torch.randn(B, L, 3, H, D, generator=g) * 0.125).to(torch.bfloat16)
     do = torch.randn(B, H, L, D, generator=g).to(torch.bfloat16)
@@ -188,7 +189,37 @@ def test_strided_views(cuda):
     got = [x.cpu() for x in (o, lse, dq, dk, dv, hq, hk, hv, hdo)]
     qc, kc, vc = (qkv[:, :, i].transpose(1, 2).contiguous() for i in range(3))
     ref = _oracle_all(qc, kc, vc, do, gq, gk, gv, scale, o=got[0], lse=got[1])
-    _compare(got, ref, torch.bfloat16, "strided")
+    _compare(got, ref, torch.bfloat16, f"strided L={L}")
+
+
+def test_wide_row_stride(cuda):
+    """Views whose row stride exceeds 16 KiB (a [B, L, 3, H, D] projection with H = 48): the persistent backward of
+    the backward cannot hold that stride in a structured buffer descriptor and takes the one-slice kernel."""
+    B, H, L, D = 1, 48, 81, 64
+    _say("row stride > 16 KiB")
+    g = torch.Generator().manual_seed(11)
+    qkv = (torch.randn(B, L, 3, H, D, generator=g) * 0.125).to(torch.bfloat16)
+    do, gq, gk, gv = (torch.randn(B, H, L, D, generator=g).to(torch.bfloat16) for _ in range(4))
+    qkv_d = qkv.to(cuda)
+    q, k, v = (qkv_d[:, :, i].transpose(1, 2) for i in range(3))
+    assert q.stride(2) * q.element_size() > 16383
+    scale = D**-0.5
+    o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do.to(cuda), scale)
+    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(
+        q, k, v, o, lse, do.to(cuda), dq, gq.to(cuda), gk.to(cuda), gv.to(cuda), scale
+    )
+    got = [x.cpu() for x in (o, lse, dq, dk, dv, hq, hk, hv, hdo)]
+    qc, kc, vc = (qkv[:, :, i].transpose(1, 2).contiguous() for i in range(3))
+    ref = _oracle_all(qc, kc, vc, do, gq, gk, gv, scale, o=got[0], lse=got[1])
+    _compare(got, ref, torch.bfloat16, "row stride > 16 KiB")
+
+
+# (B, H, L, D): more slices than the persistent kernels' grid (one workgroup per CU times the workgroups a CU holds),
+# with a remainder, for one, two and three 32-key chunks and both narrow head dims.
+@pytest.mark.parametrize("B,H,L,D", [(75, 4, 81, 64), (130, 8, 20, 64), (70, 8, 50, 32), (90, 6, 96, 32)])
+def test_persistent_many_slices(cuda, B, H, L, D):
+    _case(B, H, L, D, torch.bfloat16, cuda, seed=L)
 
 
 @pytest.mark.parametrize("L", [81, 200])
