@@ -6,6 +6,9 @@ Follows the reference's structure, restated at the size BASELINE names:
   here instead of the reference's per-cell MLP head (models/energy.py:190-201).
 - ``energy_grad`` (models/energy.py:345-350): opens the second-order window when the graph is kept, runs the energy
   forward and takes dE/dz with ``torch.autograd.grad`` (``create_graph`` for graded steps).
+- ``compiled_energy_grad`` / ``verify_compiled_energy_grad`` (models/energy.py:352-434): the same dE/dz as
+  ``torch.func.grad`` of a ``functional_call``, under ``torch.compile`` with the ``aot_eager`` backend (no Triton), and
+  the second-order probe that must agree with eager before the compiled gradient is used.
 - ``descend``: z <- z - alpha dE/dz for ``steps`` steps (the reference adds noise, rms_norm and a
   sphere projection per microstep, models/energy.py:219-241, which config 3 does not ask for).
 - ``train_step`` (config 3): ``steps`` graded descent steps, a linear decode head, cross-entropy to targets, backward.
@@ -70,10 +73,93 @@ def energy_grad(model: ScalarEnergy, v: torch.Tensor, x_emb: torch.Tensor, creat
     return g
 
 
-def descend(model, z, x_emb, steps: int, alpha: float, create_graph: bool) -> torch.Tensor:
+COMPILE_BACKEND = "aot_eager"  # a non-Triton torch.compile backend
+
+
+def compiled_energy_grad(model: ScalarEnergy):
+    """dE/dz as ``torch.func.grad`` of the energy (a ``functional_call`` over the given parameters), compiled. Call as
+    ``fn(z, x_emb, params)`` with ``params`` in ``model.named_parameters()`` order (models/energy.py:368-384)."""
+    names = [n for n, _ in model.named_parameters()]
+
+    def grad_fn(z: torch.Tensor, x_emb: torch.Tensor, params: list) -> torch.Tensor:
+        weights = dict(zip(names, params, strict=True))
+
+        def total_energy(zz: torch.Tensor) -> torch.Tensor:
+            return torch.func.functional_call(model, weights, (zz, x_emb)).sum()
+
+        return torch.func.grad(total_energy)(z)
+
+    torch._dynamo.config.cache_size_limit = max(torch._dynamo.config.cache_size_limit, 64)
+    return torch.compile(grad_fn, backend=COMPILE_BACKEND, dynamic=False)
+
+
+def verify_compiled_energy_grad(model: ScalarEnergy, compiled, v: torch.Tensor, x_emb: torch.Tensor,
+                                tol: float = 1e-3) -> dict:
+    """The reference's gate (models/energy.py:386-434): on up to two rows in float32 with a private generator, the
+    compiled dE/dz, d2E/dz2 . u and d2E/dtheta dz . u must match eager within ``tol`` (relative 2-norm), else raise.
+    Returns the three errors."""
+    rows = min(2, v.shape[0])
+    z0 = v.detach()[:rows].float()
+    x0 = x_emb.detach()[:rows].float()
+    gen = torch.Generator(device=z0.device).manual_seed(1234)
+    u = torch.randn(z0.shape, generator=gen, device=z0.device, dtype=z0.dtype)
+    params = [p for _, p in model.named_parameters()]
+
+    def probe(grad_fn):
+        z = z0.clone().requires_grad_(True)
+        with torch.enable_grad(), second_order_window(True):
+            g = grad_fn(z)
+            hz, *ht = torch.autograd.grad((g * u).sum(), [z] + params, allow_unused=True)
+        return g.detach(), hz, ht
+
+    def eager(z):
+        return torch.autograd.grad(model(z, x0).sum(), z, create_graph=True)[0]
+
+    prev = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision("highest")
+    try:
+        ref_g, ref_hz, ref_ht = probe(eager)
+        got_g, got_hz, got_ht = probe(lambda z: compiled(z, x0, params))
+    finally:
+        torch.set_float32_matmul_precision(prev)
+
+    def rel(a, r):
+        if r is None:
+            return 0.0 if a is None else float("inf")
+        if a is None:
+            return float("inf")
+        return float((a.float() - r.float()).norm() / r.float().norm().clamp_min(1e-12))
+
+    errs = {
+        "dE/dz": rel(got_g, ref_g),
+        "d2E/dz2": rel(got_hz, ref_hz),
+        "d2E/dtheta dz": max(rel(a, r) for a, r in zip(got_ht, ref_ht, strict=True)),
+    }
+    if not all(e < tol for e in errs.values()):
+        raise RuntimeError("compiled dE/dz does not match eager: " + ", ".join(f"{k}={e:.3e}" for k, e in errs.items()))
+    return errs
+
+
+def descend(model, z, x_emb, steps: int, alpha: float, create_graph: bool, compiled=None) -> torch.Tensor:
+    """``steps`` descent steps; with ``compiled`` (from ``compiled_energy_grad``) dE/dz comes from the compiled
+    function, under the same second-order window the eager path opens."""
     v = z if z.requires_grad else z.detach().requires_grad_(True)
+    params = [p for _, p in model.named_parameters()] if compiled is not None else None
+    if compiled is not None and create_graph:
+        # the attention's second-order self-test runs eagerly, before dynamo traces the module (energy.py:356-360)
+        for module in model.modules():
+            if hasattr(module, "_ensure_verified"):
+                module._ensure_verified(v.device, v.dtype)
     for _ in range(steps):
-        g = energy_grad(model, v, x_emb, create_graph)
+        if compiled is None:
+            g = energy_grad(model, v, x_emb, create_graph)
+        else:
+            with second_order_window(create_graph):
+                if create_graph:
+                    g = compiled(v, x_emb, params)
+                else:
+                    with torch.no_grad():
+                        g = compiled(v, x_emb, params)
         v = v - alpha * g
         if not create_graph:
             v = v.detach().requires_grad_(True)
@@ -89,11 +175,11 @@ class Decoder(nn.Module):
         return self.lm_head(v).float()
 
 
-def train_step(model, decoder, x, z0, targets, steps: int = 16, alpha: float = 0.1) -> torch.Tensor:
+def train_step(model, decoder, x, z0, targets, steps: int = 16, alpha: float = 0.1, compiled=None) -> torch.Tensor:
     """One config-3 training step: graded descent (create_graph), CE to ``targets``, backward. Returns the loss."""
     x_emb = model.puzzle_embedding(x, z0.dtype)
     z = z0.detach().requires_grad_(True)
-    v = descend(model, z, x_emb, steps, alpha, create_graph=True)
+    v = descend(model, z, x_emb, steps, alpha, create_graph=True, compiled=compiled)
     logits = decoder(v)
     loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1))
     loss.backward()
@@ -126,4 +212,15 @@ def build(cfg: EnergyConfig, device: torch.device, seed: int = 0):
     return model, decoder
 
 
-__all__ = ["Decoder", "EnergyConfig", "ScalarEnergy", "build", "descend", "energy_grad", "infer", "train_step"]
+__all__ = [
+    "Decoder",
+    "EnergyConfig",
+    "ScalarEnergy",
+    "build",
+    "compiled_energy_grad",
+    "descend",
+    "energy_grad",
+    "infer",
+    "train_step",
+    "verify_compiled_energy_grad",
+]
