@@ -28,7 +28,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from ebr_amd.attention import EnergyReasoningBlock, second_order_window
-from ebr_amd.layers import CastedLinear, RotaryEmbedding2D, trunc_normal_init_
+from ebr_amd.layers import CastedLinear, RotaryEmbedding2D, RotaryTable2D, trunc_normal_init_
 
 
 @dataclass
@@ -42,6 +42,7 @@ class EnergyConfig:
     attn_backend: str = "fused"
     attn_nograd_backend: str = "fused"
     rope: bool = True
+    rope_impl: str = "broadcast"  # "fused": the HIP RoPE split/merge (RotaryTable2D), reference rope_impl
 
 
 class ScalarEnergy(nn.Module):
@@ -52,7 +53,14 @@ class ScalarEnergy(nn.Module):
         self.layers = nn.ModuleList(EnergyReasoningBlock(cfg) for _ in range(cfg.num_layers))
         self.energy_head = CastedLinear(cfg.hidden_size, 1, bias=False)
         head_dim = cfg.hidden_size // cfg.num_heads
-        self.rope = RotaryEmbedding2D(head_dim, *cfg.grid) if cfg.rope else None
+        if not cfg.rope:
+            self.rope = None
+        elif cfg.rope_impl == "fused":
+            self.rope = RotaryTable2D(head_dim, *cfg.grid)
+        elif cfg.rope_impl == "broadcast":
+            self.rope = RotaryEmbedding2D(head_dim, *cfg.grid)
+        else:
+            raise ValueError(f"rope_impl must be 'broadcast' or 'fused', got {cfg.rope_impl!r}")
 
     def puzzle_embedding(self, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
         return F.embedding(x, self.embed.to(dtype))

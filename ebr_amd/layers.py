@@ -5,12 +5,14 @@ Behaviour follows reference ``models/layers.py``: ``trunc_normal_init_`` (:16-34
 requested std), ``rms_norm`` (:37-42, fp32 statistics, input dtype out), ``CastedLinear`` (:45-57, fp32 weights with
 std 1/sqrt(fan_in), cast to the input dtype), ``SwiGLU`` (:74-84, intermediate round(2/3 * expansion * hidden) rounded
 up to a multiple of 256) and the broadcast 2D RoPE (:93-143: first half of each head rotates with the cell's row,
-second half with its column).
+second half with its column). ``quarter_swap``, ``RotaryTable2D`` and ``RopeFused`` (:143-172) give the same rotation as
+full [N, D] tables for the fused RoPE split (``ebr_amd.fused_attn.rope_split``).
 """
 
 from __future__ import annotations
 
 import math
+from typing import NamedTuple
 
 import torch
 import torch.nn.functional as F
@@ -85,7 +87,7 @@ class RotaryEmbedding2D(nn.Module):
     def __init__(self, dim: int, height: int, width: int, base: float = ROPE_THETA) -> None:
         super().__init__()
         half = dim // 2
-        inv = base ** (-torch.arange(0, half, 2, dtype=torch.float32) / half)
+        inv = 1.0 / (base ** (torch.arange(0, half, 2, dtype=torch.float32) / half))  # as reference layers.py:103
         ang_h = torch.arange(height, dtype=torch.float32)[:, None] * inv[None, :]
         ang_w = torch.arange(width, dtype=torch.float32)[:, None] * inv[None, :]
         ang_h, ang_w = ang_h.repeat(1, 2), ang_w.repeat(1, 2)
@@ -114,10 +116,50 @@ def apply_rope(cos_sin, q: torch.Tensor, k: torch.Tensor):
     return rot(q), rot(k)
 
 
+class RopeFused(NamedTuple):
+    """Tables of the fused RoPE split (``rope_impl = "fused"``): fp32 [N, D] cos and signed sin."""
+
+    cos: torch.Tensor
+    sin: torch.Tensor
+
+
+def quarter_swap(x: torch.Tensor) -> torch.Tensor:
+    """The quarters (a, b, c, d) of the last dim as (b, a, d, c): rotate_half of each half without its sign."""
+    shape = x.shape
+    return x.reshape(*shape[:-1], 2, 2, shape[-1] // 4).flip(-2).reshape(shape)
+
+
+class RotaryTable2D(nn.Module):
+    """``RotaryEmbedding2D`` as full [height * width, D] tables: cell i * width + j has its row i angles in the first
+    half of D and its column j angles in the second, and rotate_half's sign is folded into sin, so the rotation is
+    ``x * cos + quarter_swap(x) * sin``."""
+
+    def __init__(self, dim: int, height: int, width: int, base: float = ROPE_THETA) -> None:
+        super().__init__()
+        if dim % 4:
+            raise ValueError(f"the fused RoPE split needs head_dim divisible by 4, got {dim}")
+        (cos_h, cos_w), (sin_h, sin_w) = RotaryEmbedding2D(dim, height, width, base)()
+        rows = torch.arange(height).repeat_interleave(width)
+        cols = torch.arange(width).repeat(height)
+        sign = torch.ones(dim)
+        sign[: dim // 4] = -1.0
+        sign[dim // 2 : dim // 2 + dim // 4] = -1.0
+        self.register_buffer("cos_table", torch.cat((cos_h[rows], cos_w[cols]), dim=-1).float(), persistent=False)
+        self.register_buffer(
+            "sin_table", (torch.cat((sin_h[rows], sin_w[cols]), dim=-1) * sign).float(), persistent=False
+        )
+
+    def forward(self) -> RopeFused:
+        return RopeFused(self.cos_table, self.sin_table)
+
+
 __all__ = [
     "RMS_NORM_EPS",
     "CastedLinear",
+    "RopeFused",
     "RotaryEmbedding2D",
+    "RotaryTable2D",
+    "quarter_swap",
     "SwiGLU",
     "apply_rope",
     "rms_norm",

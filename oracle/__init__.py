@@ -7,6 +7,7 @@ TEST INFRASTRUCTURE ONLY. Nothing in the shipped package (``ebr_amd``) imports t
 Contents:
 - ``attention_ref``: dense restatement of the reference's eager attention and of its three fused ops
   (``models/fused_attn/reference.py``, ``models/attention.py:49-54``), plus the autograd recipes that pin them.
+- ``rope_ref``: dense restatement of the fused 2D-RoPE split and merge and of their tables.
 
 Pinning (each function has at least one check that does not retype its formula):
 - ``attn_fwd``: ``torch.softmax``/``torch.logsumexp`` closed forms and known answers (L = 1, Q = 0, row shift,
@@ -17,6 +18,9 @@ Pinning (each function has at least one check that does not retype its formula):
   ``gradgradcheck``, a central finite-difference Hessian-vector check, linearity in (gQ, gK, gV) and the
   zero-cotangent special cases.
 - ``math_attention``: ``torch.nn.functional.scaled_dot_product_attention`` (fp64) and the known answers above.
+- ``rope_ref`` (the fused 2D-RoPE split/merge, ``models/fused_attn/rope_split.py:32-66``): ``ref_split`` equals the
+  textbook broadcast 2D RoPE (rotate_half per half) on the full tables and preserves each rotated pair's norm;
+  ``ref_merge`` is its exact adjoint (<split x, y> = <x, merge y> in fp64) and equals torch autograd's VJP of it.
 No function is left "parity unpinned".
 """
 
@@ -30,4 +34,12 @@ from oracle.attention_ref import (  # noqa: F401
     make_inputs,
     math_attention,
     rel_err,
+)
+from oracle.rope_ref import (  # noqa: F401,E402
+    grid_shape,
+    make_rope_inputs,
+    quarter_swap,
+    ref_merge,
+    ref_split,
+    rotary_tables,
 )

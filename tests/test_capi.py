@@ -1,4 +1,4 @@
-"""The C ABI library (no GPU needed): it loads, exports every function include/ebr_attn.h declares, reports its
+"""The C ABI library (no GPU needed): it loads, exports every function include/*.h declares, reports its
 version/arch/error texts, sizes its scratch, and rejects bad arguments before enqueueing anything.
 
 Every call below that passes placeholder pointers is constructed to fail argument validation, which runs before any
@@ -15,12 +15,14 @@ import pytest
 from ebr_amd import _capi
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "ebr_attn.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def _declared():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int64_t|int)\s+(ebr_attn_\w+)\s*\(", text, re.M)))
+    names = set()
+    for h in HEADERS:
+        names |= set(re.findall(r"^\s*(?:const\s+char\s*\*|int64_t|int)\s+(ebr_\w+)\s*\(", h.read_text(), re.M))
+    return sorted(names)
 
 
 def test_header_declares_the_expected_entry_points():
@@ -32,7 +34,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
     out = subprocess.run(["nm", "-D", "--defined-only", str(_capi.LIB_PATH)], capture_output=True, text=True).stdout
-    exported = set(re.findall(r"\b(ebr_attn_\w+)\b", out))
+    exported = set(re.findall(r"\b(ebr_(?:attn|rope)_\w+)\b", out))
     assert exported == set(_declared())
 
 
