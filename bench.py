@@ -377,9 +377,68 @@ def ebr_infer(cpu_sample_n: int):
     return out
 
 
+def rope_bench(cfg: dict, reps: int, cpu: bool) -> dict:
+    """The fused 2D-RoPE split and merge (ebr_fused::rope_split / rope_merge) at the workload's shape: qkv
+    [B, L, 3*H*D] -> q, k, v [B, H, L, D] and back. Average kernel time over ``reps`` calls on rotating inputs (HIP
+    events), achieved GB/s of the algorithmic bytes (read qkv + write q, k, v; the merge the reverse) against the
+    8 TB/s peak, and (its cpu_baseline leg) the CPU restatement timed on a small batch of the same shape."""
+    import ebr_amd.fused_attn.rope_split  # noqa: F401  (registers the ops)
+
+    B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
+    dev = torch.device("cuda", 0)
+    from ebr_amd.layers import RotaryTable2D
+
+    hgt = int(L**0.5)
+    while L % hgt:
+        hgt -= 1
+    rt = RotaryTable2D(D, hgt, L // hgt)()
+    tab = rt.cos.to(dev), rt.sin.to(dev)
+    es = torch.tensor([], dtype=dt).element_size()
+    nbytes = 2 * 3 * B * H * L * D * es
+    nsets = max(2, -(-MALL_FLUSH_BYTES // (nbytes // 2)))
+    g = torch.Generator(device=dev).manual_seed(3)
+    qkvs = [torch.randn((B, L, 3 * H * D), generator=g, device=dev).to(dt) for _ in range(nsets)]
+    none = torch.zeros(0, device=dev)
+    outs = [torch.ops.ebr_fused.rope_split(x, *tab, none, H) for x in qkvs]
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    res = {"shape": f"qkv [{B}, {L}, {3 * H * D}] <-> q, k, v [{B}, {H}, {L}, {D}] {DT_NAME[dt]}",
+           "bytes_per_call": nbytes}
+    for name, fn in (("split", lambda i: torch.ops.ebr_fused.rope_split(qkvs[i % nsets], *tab, none, H)),
+                     ("merge", lambda i: torch.ops.ebr_fused.rope_merge(*outs[i % nsets], *tab, none))):
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = ev(), ev()
+        e0.record()
+        for i in range(reps):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / roofline.PEAK_HBM_GBS, 4)}
+    if cpu:
+        import oracle
+
+        bs = 8
+        x = qkvs[0][:bs].cpu()
+        c, s_ = tab[0].cpu(), tab[1].cpu()
+        oracle.ref_split(x, c, s_, H)
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 2.0:
+            oracle.ref_split(x, c, s_, H)
+            n += 1
+        sec = (time.perf_counter() - t0) / n * (B / bs)
+        res["cpu_baseline"] = {"split_us": round(sec * 1e6, 1), "cores": torch.get_num_threads(), "kind": "port",
+                            "sample": f"the CPU restatement (oracle.ref_split) on batch {bs} of {B}, scaled linearly"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--no-ebr", action="store_true", help="skip the EBR training-step measurement (config 3)")
+    ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE split/merge measurement")
     ap.add_argument("--ebr-infer", action="store_true", help="also run the inference descent (config 4)")
     ap.add_argument("--ebr-steps", type=int, default=3)
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
@@ -499,6 +558,10 @@ def main() -> int:
         out["parity_max_rel_err"] = float(f"{err:.3e}")
     else:
         out["cpu_baseline"] = None
+    if not args.no_rope:
+        log("fused RoPE split / merge")
+        out["rope"] = rope_bench(cfg, 20, not args.no_cpu)
+        log(f"rope: {out['rope']}")
     if not args.no_ebr:
         log("EBR training step (config 3)")
         out["ebr_train"] = ebr_train(args.ebr_steps, 1, 0 if args.no_cpu else 8)
