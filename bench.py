@@ -435,10 +435,137 @@ def rope_bench(cfg: dict, reps: int, cpu: bool) -> dict:
     return res
 
 
+def descent_bench(reps: int, cpu: bool, train_steps: int) -> dict:
+    """The fused descent wrapper (ebr_fused::descent_*) at the training step's latent shape [384, 81, 512] bf16, every
+    row moving, sigma and alpha per row: each kernel's average time over ``reps`` back-to-back C-ABI launches on
+    rotating inputs (HIP events on the launch stream), achieved GB/s of its algorithmic bytes against the 8 TB/s peak;
+    the same microstep's pointwise work as eager torch formulas on the GPU; (cpu_baseline) the CPU restatement on a
+    small batch; and, with ``train_steps``, the reference microstep's graded training step with either wrapper."""
+    from ebr_amd import descent  # noqa: F401  (registers the ops)
+    from ebr_amd import energy as en
+
+    B, L, C, dt, eps = 384, 81, 512, torch.bfloat16, descent.RMS_NORM_EPS
+    dev = torch.device("cuda", 0)
+    lib = _capi.load()
+    code = _capi.DTYPE_BF16
+    S = B * L * C * 2
+    nsets = max(2, -(-MALL_FLUSH_BYTES // (3 * S)))
+    g = torch.Generator(device=dev).manual_seed(5)
+    mk = lambda: [torch.randn((B, L, C), generator=g, device=dev).to(dt) for _ in range(nsets)]  # noqa: E731
+    zs, ns, gs, dos = mk(), mk(), mk(), mk()
+    sigma = (0.05 + 0.2 * torch.rand((B, 1, 1), generator=g, device=dev)).to(dt)
+    alpha = (0.05 + 0.1 * torch.rand((B, 1, 1), generator=g, device=dev)).to(dt)
+    s32, a32 = sigma.reshape(-1).float(), alpha.reshape(-1).float()
+    vs = [torch.ops.ebr_fused.descent_noisy_point(z, n, s32, eps) for z, n in zip(zs, ns)]
+    rms = torch.empty(B, device=dev, dtype=torch.float32)
+    outs = [torch.empty_like(zs[0]) for _ in range(3)]
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: t.data_ptr()  # noqa: E731
+    calls = {
+        "noisy_point": (3 * S, lambda i: lib.ebr_descent_noisy_point(
+            code, B, L, C, eps, P(zs[i]), P(ns[i]), P(s32), P(outs[0]), sp)),
+        "step_project": (3 * S, lambda i: lib.ebr_descent_step_project(
+            code, B, L * C, eps, P(vs[i]), P(gs[i]), P(a32), None, None, P(outs[0]), P(rms), sp)),
+        "step_project_bwd": (5 * S, lambda i: lib.ebr_descent_step_project_bwd(
+            code, B, L * C, eps, P(vs[i]), P(gs[i]), P(a32), None, P(rms), P(dos[i]), P(outs[0]), P(outs[1]), None,
+            sp)),
+        "noisy_point_bwd": (3 * S, lambda i: lib.ebr_descent_noisy_point_bwd(
+            code, B, L, C, eps, P(zs[i]), P(dos[i]), P(outs[2]), sp)),
+    }  # fmt: skip
+    res = {"shape": f"latent [{B}, {L}, {C}] bf16, sigma / alpha per row, no row mask", "tensor_bytes": S}
+    total_us = 0.0
+    for name, (nbytes, fn) in calls.items():
+        for i in range(3):
+            _capi.check(fn(i % nsets), name)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            fn(i % nsets)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        total_us += us
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "gbs": round(gbs, 1),
+                     "frac_hbm": round(gbs / roofline.PEAK_HBM_GBS, 4)}
+    res["microstep_fused_us"] = round(total_us, 1)
+
+    def eager_once(i):
+        z = zs[i].detach().requires_grad_(True)
+        gg = gs[i].detach().requires_grad_(True)
+        v = en._eager_noisy_point(z, ns[i], sigma, eps)
+        out = en._eager_step_and_project(v, gg, alpha, z, None, eps)
+        return torch.autograd.grad(out, (z, gg), dos[i])
+
+    for i in range(2):
+        eager_once(i % nsets)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    n_e = max(3, reps // 4)
+    for i in range(n_e):
+        eager_once(i % nsets)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    res["microstep_eager_us"] = round(e0.elapsed_time(e1) / n_e * 1e3, 1)
+    res["speedup_vs_eager"] = round(res["microstep_eager_us"] / total_us, 2)
+    if cpu:
+        import oracle
+
+        bs = 16
+        z, n, gg, do = zs[0][:bs].cpu(), ns[0][:bs].cpu(), gs[0][:bs].cpu(), dos[0][:bs].cpu()
+        sg, al = sigma[:bs].cpu(), alpha[:bs].cpu()
+
+        def cpu_once():
+            v = oracle.noisy_point(z, n, sg, eps)
+            oracle.step_and_project(v, gg, al, z, None, eps)
+            oracle.vjp_step_and_project(v, gg, al, z, None, do, eps)
+            oracle.vjp_noisy_point(z, n, sg, do, eps)
+
+        cpu_once()
+        t0 = time.perf_counter()
+        k = 0
+        while time.perf_counter() - t0 < 2.0:
+            cpu_once()
+            k += 1
+        sec = (time.perf_counter() - t0) / k * (B / bs)
+        res["cpu_baseline"] = {"microstep_us": round(sec * 1e6, 1), "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"the CPU restatement (oracle.descent_ref forward + autograd VJPs) on batch "
+                               f"{bs} of {B}, scaled linearly"}
+    if train_steps > 0:
+        cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused")
+        model, dec = en.build(cfg, dev)
+        gc = torch.Generator("cpu").manual_seed(0)
+        x = torch.randint(0, 11, (B, L), generator=gc).to(dev)
+        z0 = torch.randn(B, L, C, generator=gc).to(dev, dt)
+        tg = torch.randint(0, 11, (B, L), generator=gc).to(dev)
+        steps = {}
+        for wrapper in ("fused", "eager"):
+            run = lambda: en.train_step(model, dec, x, z0, tg, alpha=alpha, wrapper=wrapper, sigma=sigma)  # noqa
+            run()
+            model.zero_grad(set_to_none=True)
+            dec.zero_grad(set_to_none=True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(train_steps):
+                run()
+                model.zero_grad(set_to_none=True)
+                dec.zero_grad(set_to_none=True)
+            torch.cuda.synchronize()
+            steps[wrapper] = round(train_steps / (time.perf_counter() - t0), 3)
+        res["train_step_steps_per_s"] = steps
+        res["train_step_config"] = ("config 3's network and batch with the reference microstep (rms_norm + noise, "
+                                    "sphere projection, per-row sigma / alpha), 16 graded steps")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--no-ebr", action="store_true", help="skip the EBR training-step measurement (config 3)")
     ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE split/merge measurement")
+    ap.add_argument("--no-descent", action="store_true", help="skip the fused descent-wrapper measurement")
     ap.add_argument("--ebr-infer", action="store_true", help="also run the inference descent (config 4)")
     ap.add_argument("--ebr-steps", type=int, default=3)
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
@@ -562,6 +689,10 @@ def main() -> int:
         log("fused RoPE split / merge")
         out["rope"] = rope_bench(cfg, 20, not args.no_cpu)
         log(f"rope: {out['rope']}")
+    if not args.no_descent:
+        log("fused descent wrapper")
+        out["descent"] = descent_bench(20, not args.no_cpu, 0 if args.no_ebr else 2)
+        log(f"descent: {out['descent']}")
     if not args.no_ebr:
         log("EBR training step (config 3)")
         out["ebr_train"] = ebr_train(args.ebr_steps, 1, 0 if args.no_cpu else 8)

@@ -1,4 +1,5 @@
-"""ctypes binding of ``libebr_attn.so`` (declared in ``include/ebr_attn.h`` and ``include/ebr_rope.h``).
+"""ctypes binding of ``libebr_attn.so`` (declared in ``include/ebr_attn.h``, ``include/ebr_rope.h`` and
+``include/ebr_descent.h``).
 
 The library is built in-tree by ``ebr_amd.build`` into ``ebr_amd/_lib/``. Loading needs only the HIP runtime, so the
 symbols can be checked on a machine without a GPU; every compute entry point needs a gfx950 device.
@@ -22,7 +23,7 @@ _P = ctypes.c_void_p
 _I64P = ctypes.POINTER(ctypes.c_int64)
 _F32P = ctypes.c_void_p  # fp32 device pointers are passed as raw addresses
 
-# name -> (restype, argtypes); mirrors include/ebr_attn.h and include/ebr_rope.h
+# name -> (restype, argtypes); mirrors include/ebr_attn.h, include/ebr_rope.h and include/ebr_descent.h
 SIGNATURES = {
     "ebr_attn_fwd": (
         ctypes.c_int,
@@ -51,6 +52,23 @@ SIGNATURES = {
     "ebr_rope_merge": (
         ctypes.c_int,
         [ctypes.c_int] * 5 + [_P, _I64P] * 3 + [_F32P] * 3 + [_P, _P],
+    ),
+    # include/ebr_descent.h
+    "ebr_descent_noisy_point": (
+        ctypes.c_int,
+        [ctypes.c_int] * 4 + [ctypes.c_float] + [_P, _P, _F32P, _P, _P],
+    ),
+    "ebr_descent_noisy_point_bwd": (
+        ctypes.c_int,
+        [ctypes.c_int] * 4 + [ctypes.c_float] + [_P] * 4,
+    ),
+    "ebr_descent_step_project": (
+        ctypes.c_int,
+        [ctypes.c_int] * 2 + [ctypes.c_int64, ctypes.c_float] + [_P, _P, _F32P, _P, _P, _P, _F32P, _P],
+    ),
+    "ebr_descent_step_project_bwd": (
+        ctypes.c_int,
+        [ctypes.c_int] * 2 + [ctypes.c_int64, ctypes.c_float] + [_P, _P, _F32P, _P, _F32P, _P, _P, _P, _P, _P],
     ),
     "ebr_attn_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ebr_attn_abi_version": (ctypes.c_int, []),

@@ -19,13 +19,14 @@ OUT_DIR = PKG / "_lib"
 LIB_NAME = "libebr_attn.so"
 ARCH = "gfx950"
 
-SOURCES = [CSRC / "ebr_attn.hip", CSRC / "ebr_rope.hip"]
+SOURCES = [CSRC / "ebr_attn.hip", CSRC / "ebr_rope.hip", CSRC / "ebr_descent.hip"]
 HEADERS = [
     CSRC / "attn_tiles.hpp",
     CSRC / "attn_resident.hpp",
     CSRC / "attn_long.hpp",
     ROOT / "include" / "ebr_attn.h",
     ROOT / "include" / "ebr_rope.h",
+    ROOT / "include" / "ebr_descent.h",
 ]
 
 

@@ -9,8 +9,10 @@ Follows the reference's structure, restated at the size BASELINE names:
 - ``compiled_energy_grad`` / ``verify_compiled_energy_grad`` (models/energy.py:352-434): the same dE/dz as
   ``torch.func.grad`` of a ``functional_call``, under ``torch.compile`` with the ``aot_eager`` backend (no Triton), and
   the second-order probe that must agree with eager before the compiled gradient is used.
-- ``descend``: z <- z - alpha dE/dz for ``steps`` steps (the reference adds noise, rms_norm and a
-  sphere projection per microstep, models/energy.py:219-241, which config 3 does not ask for).
+- ``descend``: z <- z - alpha dE/dz for ``steps`` steps, or, with ``wrapper``, the reference's full
+  microstep (``microstep``, models/energy.py:293-319): v = rms_norm(z) + noise, z <- where(active, sphere(v - alpha
+  dE/dv), z), its pointwise work either as the eager torch formulas (models/energy.py:219-241, the reference's
+  ``descent_wrapper_compile: false``) or as the fused HIP kernels of ``ebr_amd.descent``.
 - ``train_step`` (config 3): ``steps`` graded descent steps, a linear decode head, cross-entropy to targets, backward.
 - ``infer`` (config 4): descent without a graph over ``samples`` latents per input, then the lowest-energy sample per
   input (evaluators/protocol.py:10-12).
@@ -28,7 +30,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from ebr_amd.attention import EnergyReasoningBlock, second_order_window
-from ebr_amd.layers import CastedLinear, RotaryEmbedding2D, RotaryTable2D, trunc_normal_init_
+from ebr_amd.layers import RMS_NORM_EPS, CastedLinear, RotaryEmbedding2D, RotaryTable2D, rms_norm, trunc_normal_init_
 
 
 @dataclass
@@ -148,26 +150,102 @@ def verify_compiled_energy_grad(model: ScalarEnergy, compiled, v: torch.Tensor, 
     return errs
 
 
-def descend(model, z, x_emb, steps: int, alpha: float, create_graph: bool, compiled=None) -> torch.Tensor:
-    """``steps`` descent steps; with ``compiled`` (from ``compiled_energy_grad``) dE/dz comes from the compiled
-    function, under the same second-order window the eager path opens."""
-    v = z if z.requires_grad else z.detach().requires_grad_(True)
-    params = [p for _, p in model.named_parameters()] if compiled is not None else None
+def _gradient(model, v, x_emb, create_graph: bool, compiled, params):
+    if compiled is None:
+        return energy_grad(model, v, x_emb, create_graph)
+    with second_order_window(create_graph):
+        if create_graph:
+            return compiled(v, x_emb, params)
+        with torch.no_grad():
+            return compiled(v, x_emb, params)
+
+
+def _verify_before_compiled(model, v, compiled, create_graph: bool) -> None:
     if compiled is not None and create_graph:
         # the attention's second-order self-test runs eagerly, before dynamo traces the module (energy.py:356-360)
         for module in model.modules():
             if hasattr(module, "_ensure_verified"):
                 module._ensure_verified(v.device, v.dtype)
-    for _ in range(steps):
-        if compiled is None:
-            g = energy_grad(model, v, x_emb, create_graph)
-        else:
-            with second_order_window(create_graph):
-                if create_graph:
-                    g = compiled(v, x_emb, params)
-                else:
-                    with torch.no_grad():
-                        g = compiled(v, x_emb, params)
+
+
+# -- the descent wrapper's pointwise work as eager torch formulas (reference models/energy.py:219-241) ------------------
+
+
+def sphere(z: torch.Tensor, eps: float = RMS_NORM_EPS) -> torch.Tensor:
+    """Each row (the whole board) rescaled to unit RMS in fp32, the RMS clamped below at ``eps``. z is cast twice, as
+    the reference does, so that autograd rounds the two terms of the gradient to z's dtype separately."""
+    rms = z.float().square().mean(dim=(1, 2), keepdim=True).sqrt().clamp_min(eps)
+    return (z.float() / rms).to(z.dtype)
+
+
+def _eager_noisy_point(z, noise, sigma, eps):
+    v = rms_norm(z, eps)
+    if noise is None:
+        return v
+    return v + noise * sigma if sigma is not None else v + noise.to(dtype=v.dtype)
+
+
+def _eager_step_and_project(v, g, alpha, z, active, eps):
+    z_next = sphere(v - alpha * g, eps)
+    return z_next if active is None else torch.where(active, z_next, z.to(dtype=z_next.dtype))
+
+
+WRAPPERS = ("eager", "fused")
+
+
+def _wrapper_fns(wrapper: str):
+    if wrapper == "eager":
+        return _eager_noisy_point, _eager_step_and_project
+    if wrapper == "fused":
+        from ebr_amd import descent
+
+        def noisy(z, noise, sigma, eps):
+            if noise is None:
+                return descent.normalize(z, eps)
+            if sigma is None:
+                return descent.noisy_point_replayed(z, noise, eps)
+            return descent.noisy_point(z, noise, sigma, eps)
+
+        return noisy, descent.step_and_project
+    raise ValueError(f"wrapper must be one of {WRAPPERS}, got {wrapper!r}")
+
+
+def microstep(model, z, x_emb, *, alpha, create_graph: bool, sigma=None, noise=None, active=None,
+              wrapper: str = "fused", compiled=None, params=None, eps: float = RMS_NORM_EPS) -> torch.Tensor:
+    """One reference descent microstep (EnergyDescent.forward, models/energy.py:293-319): v = rms_norm(z) + noise
+    (``noise`` replayed as given, else drawn as randn * ``sigma`` when ``sigma`` is set, else none), g = dE/dv,
+    z' = where(active, sphere(v - alpha g), z). ``alpha``/``sigma``: a float or a per-row [B, 1, 1] tensor in z's
+    dtype; ``active``: a [B, 1, 1] bool mask or None."""
+    noisy, step = _wrapper_fns(wrapper)
+    if noise is None and sigma is not None:
+        noise = torch.randn_like(z)  # drawn eagerly, as the reference does (energy.py:331-332)
+    elif noise is not None:
+        sigma = None
+    with torch.set_grad_enabled(create_graph):
+        v = noisy(z, noise, sigma, eps)
+    if not v.requires_grad:
+        v = v.detach().requires_grad_(True)
+    g = _gradient(model, v, x_emb, create_graph, compiled, params)
+    with torch.set_grad_enabled(create_graph):
+        z_next = step(v, g, alpha, z, active, eps)
+    return z_next if create_graph else z_next.detach()
+
+
+def descend(model, z, x_emb, steps: int, alpha, create_graph: bool, compiled=None, wrapper: Optional[str] = None,
+            sigma=None, noises=None, active=None) -> torch.Tensor:
+    """``steps`` descent steps; with ``compiled`` (from ``compiled_energy_grad``) dE/dz comes from the compiled
+    function, under the same second-order window the eager path opens. ``wrapper`` None: z <- z - alpha dE/dz;
+    "eager" / "fused": the reference microstep (``microstep``) with ``sigma``, ``noises[t]`` and ``active[t]``."""
+    v = z if z.requires_grad else z.detach().requires_grad_(True)
+    params = [p for _, p in model.named_parameters()] if compiled is not None else None
+    _verify_before_compiled(model, v, compiled, create_graph)
+    for t in range(steps):
+        if wrapper is not None:
+            v = microstep(model, v, x_emb, alpha=alpha, create_graph=create_graph, sigma=sigma,
+                          noise=None if noises is None else noises[t], active=None if active is None else active[t],
+                          wrapper=wrapper, compiled=compiled, params=params)
+            continue
+        g = _gradient(model, v, x_emb, create_graph, compiled, params)
         v = v - alpha * g
         if not create_graph:
             v = v.detach().requires_grad_(True)
@@ -183,11 +261,14 @@ class Decoder(nn.Module):
         return self.lm_head(v).float()
 
 
-def train_step(model, decoder, x, z0, targets, steps: int = 16, alpha: float = 0.1, compiled=None) -> torch.Tensor:
-    """One config-3 training step: graded descent (create_graph), CE to ``targets``, backward. Returns the loss."""
+def train_step(model, decoder, x, z0, targets, steps: int = 16, alpha=0.1, compiled=None,
+               wrapper: Optional[str] = None, sigma=None, noises=None, active=None) -> torch.Tensor:
+    """One config-3 training step: graded descent (create_graph), CE to ``targets``, backward. Returns the loss.
+    ``wrapper`` and the rest select the reference microstep (``descend``)."""
     x_emb = model.puzzle_embedding(x, z0.dtype)
     z = z0.detach().requires_grad_(True)
-    v = descend(model, z, x_emb, steps, alpha, create_graph=True, compiled=compiled)
+    v = descend(model, z, x_emb, steps, alpha, create_graph=True, compiled=compiled, wrapper=wrapper, sigma=sigma,
+                noises=noises, active=active)
     logits = decoder(v)
     loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1))
     loss.backward()
@@ -229,6 +310,8 @@ __all__ = [
     "descend",
     "energy_grad",
     "infer",
+    "microstep",
+    "sphere",
     "train_step",
     "verify_compiled_energy_grad",
 ]
