@@ -285,6 +285,19 @@ def pmc_target(cfg: dict, reps: int = 3) -> None:
         log(f"pmc target: {p} algorithmic bytes per launch {roofline.phase_bytes(p, B, H, L, D, es):.0f}")
 
 
+def descent_target(reps: int = 20) -> None:
+    """The descent-wrapper leg alone, for ``rocprofv3`` (kernel trace and --pmc passes): the same 256 MiB calibration
+    copy as ``pmc_target``, then ``descent_bench``'s timed launches; prints its JSON."""
+    dev = torch.device("cuda", 0)
+    src = torch.empty(64 << 20, device=dev, dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    print(json.dumps(descent_bench(reps, False, 0)), flush=True)
+
+
 def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
     """BASELINE config 3: 2 post-norm blocks, hidden 512, 8 x 64 heads, SwiGLU x4, mean-pooled linear energy head;
     x ~ U{0..10} [384, 81]; z ~ N(0, 1) [384, 81, 512]; 16 steps z <- z - 0.1 dE/dz with create_graph; CE of a linear
@@ -569,6 +582,7 @@ def main() -> int:
     ap.add_argument("--ebr-infer", action="store_true", help="also run the inference descent (config 4)")
     ap.add_argument("--ebr-steps", type=int, default=3)
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
+    ap.add_argument("--descent-target", action="store_true", help="run only the descent-wrapper leg (for rocprofv3)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
@@ -594,6 +608,9 @@ def main() -> int:
     _capi.load()
     import ebr_amd.fused_attn.ops  # noqa: F401
 
+    if args.descent_target:
+        descent_target()
+        return 0
     cfg = CONFIGS[args.config]
     if args.pmc_target:
         pmc_target(cfg)
