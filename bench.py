@@ -285,6 +285,30 @@ def pmc_target(cfg: dict, reps: int = 3) -> None:
         log(f"pmc target: {p} algorithmic bytes per launch {roofline.phase_bytes(p, B, H, L, D, es):.0f}")
 
 
+MULTI_SOLUTION_SHAPES = [(768, 4, 28, 128), (768, 4, 45, 128), (768, 4, 64, 128), (768, 4, 100, 128)]
+
+
+def multi_solution_bench(steps: int, warmup: int) -> dict:
+    """The multi-solution recipes' attention shapes (hidden 512 over 4 heads, D = 128, global batch 768; L = 28 and 45
+    for graph colouring 8 / 10, 64 and 100 for N-Queens 8 / 10), bf16: per-phase event times of the same fwd -> bwd ->
+    bwd_bwd step on rotating input sets, and the step's fraction of its attainable roofline."""
+    dev = torch.device("cuda", 0)
+    out = {}
+    for B, H, L, D in MULTI_SOLUTION_SHAPES:
+        cfg = dict(name=f"B={B} H={H} L={L} D={D}", B=B, H=H, L=L, D=D, dtype=torch.bfloat16, qkv_scale=0.125)
+        sets = make_sets(cfg, dev, max(2, -(-MALL_FLUSH_BYTES // (7 * B * H * L * D * 2))))
+        scale = D**-0.5
+        ms, ph = time_steps(sets, scale, steps, warmup)
+        roof = sum(roofline.roof_time_s(p, B, H, L, D, 2, "bf16") for p in PHASES)
+        flops = sum(roofline.phase_flops(p, B, H, L, D) for p in PHASES)
+        out[f"L{L}"] = {"ms_per_step": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                        "pct_attainable_roofline": round(100 * roof / (ms * 1e-3), 1),
+                        **{f"{p}_us": round(ph[p] * 1e3, 1) for p in PHASES}}
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
 def descent_target(reps: int = 20) -> None:
     """The descent-wrapper leg alone, for ``rocprofv3`` (kernel trace and --pmc passes): the same 256 MiB calibration
     copy as ``pmc_target``, then ``descent_bench``'s timed launches; prints its JSON."""
@@ -579,6 +603,7 @@ def main() -> int:
     ap.add_argument("--no-ebr", action="store_true", help="skip the EBR training-step measurement (config 3)")
     ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE split/merge measurement")
     ap.add_argument("--no-descent", action="store_true", help="skip the fused descent-wrapper measurement")
+    ap.add_argument("--no-multi", action="store_true", help="skip the multi-solution (D = 128) attention shapes")
     ap.add_argument("--ebr-infer", action="store_true", help="also run the inference descent (config 4)")
     ap.add_argument("--ebr-steps", type=int, default=3)
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
@@ -706,6 +731,10 @@ def main() -> int:
         log("fused RoPE split / merge")
         out["rope"] = rope_bench(cfg, 20, not args.no_cpu)
         log(f"rope: {out['rope']}")
+    if not args.no_multi:
+        log("multi-solution attention shapes (D = 128)")
+        out["multi_solution"] = multi_solution_bench(10, 3)
+        log(f"multi-solution: {out['multi_solution']}")
     if not args.no_descent:
         log("fused descent wrapper")
         out["descent"] = descent_bench(20, not args.no_cpu, 0 if args.no_ebr else 2)

@@ -153,6 +153,14 @@ def test_config1_sudoku_bf16_full_size(cuda):
     _sampled(768, 8, 81, 64, torch.bfloat16, cuda, 128)
 
 
+@pytest.mark.parametrize("L", [28, 45, 64, 100])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_multi_solution_head_dim_128_full_size(cuda, L, dtype):
+    """The multi-solution recipes' shapes: hidden 512 over 4 heads (D = 128), global batch 768, L = 28 / 45 (graph
+    colouring 8 / 10), 64 / 100 (N-Queens 8 / 10); 16 random slices checked."""
+    _sampled(768, 4, L, 128, dtype, cuda, 16, seed=L)
+
+
 def test_config2_maze_bf16_full_size(cuda):
     """Config 2: bf16 B=64 H=8 L=900 D=64 at full size; 12 random slices checked."""
     _sampled(64, 8, 900, 64, torch.bfloat16, cuda, 12)
