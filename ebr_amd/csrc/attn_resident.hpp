@@ -26,7 +26,10 @@ template <int DP> struct Sw {
         if constexpr (DP == 32) {
             return (x >> 2) & 3;
         } else if constexpr (DP == 64) {
-            return (x & 7) ^ ((x >> 3) & 1);
+            // bits 1 and 2 of x swapped: with 4 or more waves per CU, the A-operand reads of 16 rows x 2 chunk
+            // positions then meet no bank conflict (measured with SQ_LDS_BANK_CONFLICT; the earlier
+            // (x & 7) ^ (x >> 3 & 1) cost a quarter of the read cycles), and the transposed reads stay conflict-free
+            return (x & 1) | ((x & 4) >> 1) | ((x & 2) << 1);
         } else {
             return x & 15;
         }
