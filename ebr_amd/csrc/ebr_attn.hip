@@ -46,12 +46,12 @@ struct Args {
     int xcd_remap;  // 1: keep the blocks of one (b, h) on one XCD
     Strided q, k, v, dO, gq, gk, gv;
     const void* o;      // contiguous [B, H, L, D]
-    const float* lse;   // contiguous [B, H, L]
+    const float* lse;   // contiguous [B, H, L] (fp64 kernels read it as double)
     void* out0;
     void* out1;
     void* out2;
     void* out3;
-    float* lse_out;
+    float* lse_out;     // (fp64 kernels write it as double)
     float* stats;       // [3][B * H * L] fp32: Dr, E, T (two-launch shapes only)
     int64_t bhl;        // B * H * L
 };
@@ -753,7 +753,7 @@ static int fused_threads(int L) {
     return t < MIN_THREADS ? MIN_THREADS : t;
 }
 
-static int elem_size(int dtype) { return dtype == EBR_DTYPE_F32 ? 4 : 2; }
+static int elem_size(int dtype) { return dtype == EBR_DTYPE_F64 ? 8 : (dtype == EBR_DTYPE_F32 ? 4 : 2); }
 
 // The resident one-workgroup kernels (16-bit inputs): D must be a full chunk width and every slice's byte range
 // (rows 0 .. L-1 of each strided input) must be addressable with 32-bit buffer offsets.
@@ -779,17 +779,21 @@ static bool struct_strides_fit(const Args& a) {
 }
 
 static int check_shape(int dtype, int B, int H, int L, int D) {
-    if (dtype != EBR_DTYPE_F32 && dtype != EBR_DTYPE_BF16 && dtype != EBR_DTYPE_F16) return EBR_ERR_DTYPE;
+    if (dtype != EBR_DTYPE_F32 && dtype != EBR_DTYPE_BF16 && dtype != EBR_DTYPE_F16 && dtype != EBR_DTYPE_F64)
+        return EBR_ERR_DTYPE;
     if (B < 1 || H < 1 || L < 1 || D < 1 || D > 128) return EBR_ERR_SHAPE;
-    const int vec = dtype == EBR_DTYPE_F32 ? 4 : 8;
+    const int vec = dtype == EBR_DTYPE_F64 ? 1 : (dtype == EBR_DTYPE_F32 ? 4 : 8);
     if (D % vec) return EBR_ERR_SHAPE;
     if ((int64_t)B * H * L >= ((int64_t)1 << 31)) return EBR_ERR_SHAPE;
     return EBR_OK;
 }
 
+// Row starts must be 16-byte aligned, except for fp64 (element-wise kernels): 8-byte aligned elements.
+static int row_align(int es) { return es == 8 ? 8 : 16; }
+
 static int check_ptr(const void* p, int es, bool need) {
     if (!p) return need ? EBR_ERR_NULL : EBR_OK;
-    return ((uintptr_t)p % 16) ? EBR_ERR_ALIGN : EBR_OK;
+    return ((uintptr_t)p % row_align(es)) ? EBR_ERR_ALIGN : EBR_OK;
 }
 
 static int check_strided(const void* p, const int64_t* s, int es) {
@@ -797,7 +801,7 @@ static int check_strided(const void* p, const int64_t* s, int es) {
     if (rc) return rc;
     if (!s) return EBR_ERR_NULL;
     for (int i = 0; i < 3; ++i)
-        if (s[i] < 0 || ((s[i] * es) % 16)) return EBR_ERR_ALIGN;
+        if (s[i] < 0 || ((s[i] * es) % row_align(es))) return EBR_ERR_ALIGN;
     return EBR_OK;
 }
 
@@ -845,6 +849,8 @@ static int persistent_grid(const void* kernel, int threads, int64_t work) {
     }
     return (int)(work < slots ? work : slots);
 }
+
+#include "attn_f64.hpp"
 
 template <template <typename, int> class F, typename... Rest>
 static int dispatch(int dtype, int D, Rest&&... rest) {
@@ -1073,11 +1079,12 @@ const char* ebr_attn_arch(void) { return "gfx950"; }
 const char* ebr_attn_error_string(int code) {
     switch (code) {
         case EBR_OK: return "ok";
-        case EBR_ERR_DTYPE: return "unsupported dtype (expected fp32, bf16 or fp16)";
+        case EBR_ERR_DTYPE: return "unsupported dtype (expected fp32, bf16, fp16 or fp64)";
         case EBR_ERR_SHAPE:
             return "unsupported shape (need B, H, L >= 1, B*H*L < 2^31, D <= 128 and a multiple of 8 for 16-bit "
                    "or 4 for fp32)";
-        case EBR_ERR_ALIGN: return "row start not 16-byte aligned (base pointer or a B/H/L stride)";
+        case EBR_ERR_ALIGN:
+            return "row start not 16-byte aligned (8-byte for fp64) (base pointer or a B/H/L stride)";
         case EBR_ERR_NULL: return "required pointer is NULL";
         case EBR_ERR_SCRATCH: return "scratch buffer required for this shape but NULL";
         default: break;
@@ -1086,7 +1093,7 @@ const char* ebr_attn_error_string(int code) {
     return "unknown error code";
 }
 
-int64_t ebr_attn_scratch_bytes(int op, int B, int H, int L, int D) {
+int64_t ebr_attn_scratch_bytes(int op, int B, int H, int L, int D) {  // fp64 calls need none
     (void)D;
     if (B < 1 || H < 1 || L < 1) return 0;
     if (fused_shape(L)) return 0;
@@ -1097,7 +1104,7 @@ int64_t ebr_attn_scratch_bytes(int op, int B, int H, int L, int D) {
 }
 
 int ebr_attn_fwd(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
-                 const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], void* o, float* lse,
+                 const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], void* o, void* lse,
                  void* stream) {
     int rc = check_shape(dtype, B, H, L, D);
     if (rc) return rc;
@@ -1110,13 +1117,14 @@ int ebr_attn_fwd(int dtype, int B, int H, int L, int D, float scale, const void*
     a.k = mk(k, k_str);
     a.v = mk(v, v_str);
     a.out0 = o;
-    a.lse_out = lse;
+    a.lse_out = static_cast<float*>(lse);
+    if (dtype == EBR_DTYPE_F64) return f64_fwd(a, (hipStream_t)stream);
     return dispatch<FwdLaunch>(dtype, D, a, (hipStream_t)stream);
 }
 
 int ebr_attn_bwd(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
                  const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], const void* o,
-                 const float* lse, const void* dO, const int64_t dO_str[3], void* dq, void* dk, void* dv,
+                 const void* lse, const void* dO, const int64_t dO_str[3], void* dq, void* dk, void* dv,
                  float* scratch, void* stream) {
     int rc = check_shape(dtype, B, H, L, D);
     if (rc) return rc;
@@ -1126,24 +1134,26 @@ int ebr_attn_bwd(int dtype, int B, int H, int L, int D, float scale, const void*
         (rc = check_ptr(o, es, true)) || (rc = check_ptr(lse, 4, true)) || (rc = check_ptr(dq, es, true)) ||
         (rc = check_ptr(dk, es, true)) || (rc = check_ptr(dv, es, true)))
         return rc;
-    if (ebr_attn_scratch_bytes(EBR_OP_BWD, B, H, L, D) > 0 && !scratch) return EBR_ERR_SCRATCH;
+    if (dtype != EBR_DTYPE_F64 && ebr_attn_scratch_bytes(EBR_OP_BWD, B, H, L, D) > 0 && !scratch)
+        return EBR_ERR_SCRATCH;
     Args a = base_args(B, H, L, D, scale);
     a.q = mk(q, q_str);
     a.k = mk(k, k_str);
     a.v = mk(v, v_str);
     a.dO = mk(dO, dO_str);
     a.o = o;
-    a.lse = lse;
+    a.lse = static_cast<const float*>(lse);
     a.out0 = dq;
     a.out1 = dk;
     a.out2 = dv;
     a.stats = scratch;
+    if (dtype == EBR_DTYPE_F64) return f64_bwd(a, (hipStream_t)stream);
     return dispatch<BwdLaunch>(dtype, D, a, (hipStream_t)stream);
 }
 
 int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
                      const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], const void* o,
-                     const float* lse, const void* dO, const int64_t dO_str[3], const void* gq,
+                     const void* lse, const void* dO, const int64_t dO_str[3], const void* gq,
                      const int64_t gq_str[3], const void* gk, const int64_t gk_str[3], const void* gv,
                      const int64_t gv_str[3], void* hq, void* hk, void* hv, void* hdo, float* scratch,
                      void* stream) {
@@ -1157,7 +1167,8 @@ int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale, const v
         (rc = check_ptr(hq, es, true)) || (rc = check_ptr(hk, es, true)) || (rc = check_ptr(hv, es, true)) ||
         (rc = check_ptr(hdo, es, true)))
         return rc;
-    if (ebr_attn_scratch_bytes(EBR_OP_BWD_BWD, B, H, L, D) > 0 && !scratch) return EBR_ERR_SCRATCH;
+    if (dtype != EBR_DTYPE_F64 && ebr_attn_scratch_bytes(EBR_OP_BWD_BWD, B, H, L, D) > 0 && !scratch)
+        return EBR_ERR_SCRATCH;
     Args a = base_args(B, H, L, D, scale);
     a.q = mk(q, q_str);
     a.k = mk(k, k_str);
@@ -1167,12 +1178,13 @@ int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale, const v
     a.gk = mk(gk, gk_str);
     a.gv = mk(gv, gv_str);
     a.o = o;
-    a.lse = lse;
+    a.lse = static_cast<const float*>(lse);
     a.out0 = hq;
     a.out1 = hk;
     a.out2 = hv;
     a.out3 = hdo;
     a.stats = scratch;
+    if (dtype == EBR_DTYPE_F64) return f64_bwd_bwd(a, (hipStream_t)stream);
     return dispatch<BbLaunch>(dtype, D, a, (hipStream_t)stream);
 }
 

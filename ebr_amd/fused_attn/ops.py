@@ -25,7 +25,12 @@ from ebr_amd.fused_attn.loader import hip_library
 
 Tensor = torch.Tensor
 
-_DTYPE_CODE = {torch.float32: _capi.DTYPE_F32, torch.bfloat16: _capi.DTYPE_BF16, torch.float16: _capi.DTYPE_F16}
+_DTYPE_CODE = {
+    torch.float32: _capi.DTYPE_F32,
+    torch.bfloat16: _capi.DTYPE_BF16,
+    torch.float16: _capi.DTYPE_F16,
+    torch.float64: _capi.DTYPE_F64,
+}
 
 
 def default_scale(q: Tensor, scale: Optional[float]) -> float:
@@ -34,7 +39,7 @@ def default_scale(q: Tensor, scale: Optional[float]) -> float:
 
 
 def lse_dtype_for(x: Tensor) -> torch.dtype:
-    """lse is fp32 (reference reference.py:14-16 keeps fp64 for fp64 inputs, which these kernels do not take)."""
+    """lse is fp32; fp64 inputs keep fp64 (reference reference.py:14-16)."""
     return torch.float64 if x.dtype == torch.float64 else torch.float32
 
 
@@ -62,16 +67,23 @@ def _check(q: Tensor, k: Tensor, v: Tensor) -> None:
 def _dtype_code(t: Tensor) -> int:
     code = _DTYPE_CODE.get(t.dtype)
     if code is None:
-        raise TypeError(f"fused attention: unsupported dtype {t.dtype} (gfx950 kernels take float32, bfloat16, float16)")
+        raise TypeError(
+            f"fused attention: unsupported dtype {t.dtype} (gfx950 kernels take float32, bfloat16, float16, float64)"
+        )
     return code
 
 
+def _align(t: Tensor) -> int:
+    """Row-start alignment the kernels need: 16 bytes, or the element (8 bytes) for the fp64 kernels."""
+    return 8 if t.dtype == torch.float64 else 16
+
+
 def _rows(t: Tensor) -> Tensor:
-    """Keep any B/H/L strides (views of a fused qkv projection, expanded zero rows) when every row start is 16-byte
-    aligned and D is unit-stride; otherwise copy (reference triton_kernels.py:598-601 keeps unit-D views)."""
-    es = t.element_size()
-    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0
-    ok = ok and all(s >= 0 and (s * es) % 16 == 0 for s in t.stride()[:3])
+    """Keep any B/H/L strides (views of a fused qkv projection, expanded zero rows) when every row start is aligned
+    and D is unit-stride; otherwise copy (reference triton_kernels.py:598-601 keeps unit-D views)."""
+    es, al = t.element_size(), _align(t)
+    ok = t.stride(-1) == 1 and t.data_ptr() % al == 0
+    ok = ok and all(s >= 0 and (s * es) % al == 0 for s in t.stride()[:3])
     return t if ok else t.contiguous()
 
 
@@ -84,6 +96,8 @@ def _stream(t: Tensor) -> ctypes.c_void_p:
 
 
 def _scratch(op: int, q: Tensor) -> Tuple[Optional[Tensor], int]:
+    if q.dtype == torch.float64:  # the fp64 kernels need none
+        return None, 0
     B, H, L, D = q.shape
     nbytes = int(hip_library().ebr_attn_scratch_bytes(op, B, H, L, D))
     if nbytes <= 0:
@@ -105,7 +119,7 @@ def attn_fwd(q: Tensor, k: Tensor, v: Tensor, scale: float) -> Tuple[Tensor, Ten
     q, k, v = _rows(q), _rows(k), _rows(v)
     B, H, L, D = q.shape
     o = torch.empty((B, H, L, D), device=q.device, dtype=q.dtype)
-    lse = torch.empty((B, H, L), device=q.device, dtype=torch.float32)
+    lse = torch.empty((B, H, L), device=q.device, dtype=lse_dtype_for(q))
     with torch.cuda.device(q.device):
         rc = lib.ebr_attn_fwd(
             code, B, H, L, D, ctypes.c_float(scale),
@@ -132,7 +146,7 @@ def attn_bwd(
     lib = hip_library()
     code = _dtype_code(q)
     q, k, v, do = _rows(q), _rows(k), _rows(v), _rows(do)
-    o, lse = _contig(o.to(q.dtype)), _contig(lse.to(torch.float32))
+    o, lse = _contig(o.to(q.dtype)), _contig(lse.to(lse_dtype_for(q)))
     B, H, L, D = q.shape
     dq, dk, dv = (torch.empty((B, H, L, D), device=q.device, dtype=q.dtype) for _ in range(3))
     scratch, sp = _scratch(_capi.OP_BWD, q)
@@ -177,7 +191,7 @@ def attn_bwd_bwd(
     q, k, v = _rows(q), _rows(k), _rows(v)
     do = _rows(do.to(q.dtype))
     gq, gk, gv = _rows(gq.to(q.dtype)), _rows(gk.to(q.dtype)), _rows(gv.to(q.dtype))
-    o, lse = _contig(o.to(q.dtype)), _contig(lse.to(torch.float32))
+    o, lse = _contig(o.to(q.dtype)), _contig(lse.to(lse_dtype_for(q)))
     B, H, L, D = q.shape
     hq, hk, hv, hdo = (torch.empty((B, H, L, D), device=q.device, dtype=q.dtype) for _ in range(4))
     scratch, sp = _scratch(_capi.OP_BWD_BWD, q)

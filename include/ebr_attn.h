@@ -5,18 +5,22 @@
  * meaning; only the calling convention is C (plain pointers, sizes and strides, no framework types).
  *
  * Conventions shared by every entry point:
- *   - dtype: EBR_DTYPE_F32, EBR_DTYPE_BF16 or EBR_DTYPE_F16; all tensor arguments of one call share it, except
- *     lse and the scratch, which are always fp32.
+ *   - dtype: EBR_DTYPE_F32, EBR_DTYPE_BF16, EBR_DTYPE_F16 or EBR_DTYPE_F64; all tensor arguments of one call share
+ *     it, except lse and the scratch: lse is fp32 (fp64 for EBR_DTYPE_F64, as the reference keeps fp64 for fp64
+ *     inputs, reference.py:14-16), the scratch fp32.
  *   - Strided inputs pass their element strides for the B, H and L dimensions as int64_t[3]; the D dimension is
  *     unit-stride. A stride may be 0 (an expanded row, e.g. an all-zero cotangent). Every row start must be 16-byte
- *     aligned: base pointer 16-byte aligned and each stride a multiple of 16 bytes.
- *   - o, lse and every output are contiguous [B, H, L, D] (lse: [B, H, L], fp32, natural log).
+ *     aligned: base pointer 16-byte aligned and each stride a multiple of 16 bytes (fp64: 8 bytes, i.e. any
+ *     element-aligned view).
+ *   - o, lse and every output are contiguous [B, H, L, D] (lse: [B, H, L], natural log).
  *   - scale is the softmax scale (D ** -0.5 by default), already rounded to fp32.
  *   - stream is a hipStream_t (NULL = the null stream). Kernels are enqueued on it; nothing synchronises.
  *   - The caller owns every buffer; the library allocates nothing and keeps no pointer after returning.
  *   - Return value: 0 on success, otherwise an EBR_ERR_* code or EBR_ERR_HIP_BASE + hipError_t;
  *     ebr_attn_error_string() describes it. Argument checks run before anything is enqueued.
- *   - Supported shapes: B, H, L >= 1; D a multiple of 8 (16-bit) or 4 (fp32) with D <= 128.
+ *   - Supported shapes: B, H, L >= 1; D <= 128 and a multiple of 8 (16-bit) or 4 (fp32); any D for fp64.
+ *   - fp64 runs exact fp64 vector-ALU kernels (the reference's fp64 path serves gradcheck shapes) and needs no
+ *     scratch.
  */
 #ifndef EBR_ATTN_H
 #define EBR_ATTN_H
@@ -27,12 +31,13 @@
 extern "C" {
 #endif
 
-#define EBR_ATTN_ABI_VERSION 1
+#define EBR_ATTN_ABI_VERSION 2
 
 enum {
     EBR_DTYPE_F32 = 0,
     EBR_DTYPE_BF16 = 1,
     EBR_DTYPE_F16 = 2,
+    EBR_DTYPE_F64 = 3,
 };
 
 enum {
@@ -58,7 +63,7 @@ int ebr_attn_fwd(int dtype, int B, int H, int L, int D, float scale,
                  const void* q, const int64_t q_str[3],
                  const void* k, const int64_t k_str[3],
                  const void* v, const int64_t v_str[3],
-                 void* o, float* lse, void* stream);
+                 void* o, void* lse, void* stream);
 
 /* Backward: (dq, dk, dv) = gradient of <dO, o> with respect to (q, k, v); rowsum(dO * o) uses the stored o.
  * Replaces ebr_fused::attn_bwd(q, k, v, o, lse, do, scale) -> (dq, dk, dv)
@@ -68,7 +73,7 @@ int ebr_attn_bwd(int dtype, int B, int H, int L, int D, float scale,
                  const void* q, const int64_t q_str[3],
                  const void* k, const int64_t k_str[3],
                  const void* v, const int64_t v_str[3],
-                 const void* o, const float* lse,
+                 const void* o, const void* lse,
                  const void* dO, const int64_t dO_str[3],
                  void* dq, void* dk, void* dv, float* scratch, void* stream);
 
@@ -81,7 +86,7 @@ int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale,
                      const void* q, const int64_t q_str[3],
                      const void* k, const int64_t k_str[3],
                      const void* v, const int64_t v_str[3],
-                     const void* o, const float* lse,
+                     const void* o, const void* lse,
                      const void* dO, const int64_t dO_str[3],
                      const void* gq, const int64_t gq_str[3],
                      const void* gk, const int64_t gk_str[3],

@@ -171,7 +171,8 @@ def test_argument_errors():
     with pytest.raises(ValueError):
         ops._check(q[0], q[0], q[0])
     with pytest.raises(TypeError):
-        ops._dtype_code(q.double())
+        ops._dtype_code(q.to(torch.int32))
+    assert ops._dtype_code(q.double()) == 3  # fp64 has kernels of its own
     assert ops.default_scale(q, None) == 8**-0.5 and ops.default_scale(q, 0.3) == 0.3
 
 
@@ -181,6 +182,8 @@ def test_rows_keeps_aligned_views_and_copies_others():
     assert ops._rows(q) is q
     odd = torch.zeros(2, 3, 5, 65, dtype=torch.bfloat16)[..., :64]  # row stride 65 elements: not 16-byte aligned
     assert ops._rows(odd) is not odd and ops._rows(odd).is_contiguous()
+    odd64 = torch.zeros(2, 3, 5, 65, dtype=torch.float64)[..., :64]  # fp64 needs element alignment only
+    assert ops._rows(odd64) is odd64
 
 
 def test_loader_modes(monkeypatch):

@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_arch_and_error_texts():
     lib = _capi.load()
-    assert lib.ebr_attn_abi_version() == _capi.ABI_VERSION == 1
+    assert lib.ebr_attn_abi_version() == _capi.ABI_VERSION == 2
     assert lib.ebr_attn_arch() == b"gfx950"
     for code in (0, 1, 2, 3, 4, 5):
         assert lib.ebr_attn_error_string(code)
@@ -74,8 +74,10 @@ def _fwd(dtype=1, B=1, H=1, L=4, D=64, q=P, qs=(0, 0, 64), o=P, lse=P):
 @pytest.mark.parametrize(
     "kwargs,code",
     [
-        (dict(dtype=3), 1),  # fp64 / unknown dtype
+        (dict(dtype=4), 1),  # unknown dtype
         (dict(dtype=-1), 1),
+        (dict(dtype=3, D=129), 2),  # fp64: any D up to 128
+        (dict(dtype=3, q=P + 4), 3),  # fp64 rows need 8-byte alignment
         (dict(D=136), 2),  # D > 128
         (dict(D=60), 2),  # not a multiple of 8 for bf16
         (dict(dtype=0, D=62), 2),  # not a multiple of 4 for fp32

@@ -308,7 +308,7 @@ def test_bad_arguments_raise(cuda):
     with pytest.raises(ValueError):
         torch.ops.ebr_fused.attn_fwd(q, q.half(), q, 0.125)
     with pytest.raises(TypeError):
-        torch.ops.ebr_fused.attn_fwd(q.double(), q.double(), q.double(), 0.125)
+        torch.ops.ebr_fused.attn_fwd(q.to(torch.int32), q.to(torch.int32), q.to(torch.int32), 0.125)
     with pytest.raises(ValueError):  # D > 128
         x = torch.randn(1, 1, 4, 136, device=cuda)
         torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
