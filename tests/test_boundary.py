@@ -224,6 +224,26 @@ def test_verify_second_order_rejects_backend_without_second_derivative():
         att.verify_second_order(bad, device=torch.device("cpu"))
 
 
+def test_self_test_priming_keeps_the_global_rng_and_seeding_reaches_every_layer():
+    """prime_attention_self_test runs each layer's self-test once under a forked RNG (the caller's next draw is
+    unchanged); seed_attention_self_test sets the seed the pending self-tests will use."""
+    from ebr_amd import energy as en
+
+    cfg = en.EnergyConfig(hidden_size=32, num_heads=2, num_layers=2, grid=(3, 3), attn_backend="math",
+                          attn_nograd_backend="math")
+    model, _ = en.build(cfg, torch.device("cpu"), seed=1)
+    layers = [m for m in model.modules() if isinstance(m, att.EnergyAttention)]
+    assert len(layers) == 2
+    att.seed_attention_self_test(model, 1234)
+    assert all(m.self_test_seed == 1234 for m in layers)
+    torch.manual_seed(7)
+    expected = torch.rand(3)
+    torch.manual_seed(7)
+    att.prime_attention_self_test(model)
+    assert all(m._verified for m in layers)
+    assert torch.equal(torch.rand(3), expected)
+
+
 def test_backend_registry_and_tier_flag():
     assert set(att.ATTENTION_BACKENDS) == {"math", "sdpa_auto", "fused"}
     assert att.get_backend("fused").second_order and not att.get_backend("sdpa_auto").second_order
