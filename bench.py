@@ -331,7 +331,8 @@ def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
 
     B, L, V = 384, 81, 11
     dev = torch.device("cuda", 0)
-    cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused")
+    # the fused 2D RoPE split/merge, as the reference's Sudoku recipe sets it (config/train/sudoku.yaml:11)
+    cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused", rope_impl="fused")
     model, dec = en.build(cfg, dev)
     g = torch.Generator("cpu").manual_seed(0)
     x = torch.randint(0, V, (B, L), generator=g).to(dev)
@@ -352,7 +353,8 @@ def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     out = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 2), "loss": round(float(loss), 4),
-           "config": "B=384 L=81 hidden=512 heads=8x64 layers=2 SwiGLU x4, 16 create_graph descent steps, bf16",
+           "config": "B=384 L=81 hidden=512 heads=8x64 layers=2 SwiGLU x4, 16 create_graph descent steps, bf16; 2D RoPE "
+                     "by the fused split/merge (the reference's Sudoku recipe); CPU: the broadcast RoPE",
            "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 2**30, 1)}
     if cpu_sample_b > 0:
         cores = len(os.sched_getaffinity(0))
@@ -572,7 +574,7 @@ def descent_bench(reps: int, cpu: bool, train_steps: int) -> dict:
                                "sample": f"the CPU restatement (oracle.descent_ref forward + autograd VJPs) on batch "
                                f"{bs} of {B}, scaled linearly"}
     if train_steps > 0:
-        cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused")
+        cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused", rope_impl="fused")
         model, dec = en.build(cfg, dev)
         gc = torch.Generator("cpu").manual_seed(0)
         x = torch.randint(0, 11, (B, L), generator=gc).to(dev)
