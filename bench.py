@@ -235,7 +235,8 @@ def bb_kernel_name(cfg: dict) -> str:
     L, D, dt = cfg["L"], cfg["D"], cfg["dtype"]
     if L > 128:
         if dt != torch.float32 and D in (32, 64):
-            return f"k_bb_long_row<{DT_NAME[dt]}, {D}, 4, 64> + k_bb_long_col<{DT_NAME[dt]}, {D}, 4>"
+            nw = 7 if cfg["B"] * cfg["H"] * -(-L // 112) >= 1024 else 4  # long_wide() in ebr_attn.hip
+            return f"k_bb_long_row<{DT_NAME[dt]}, {D}, {nw}, 64> + k_bb_long_col<{DT_NAME[dt]}, {D}, {nw}>"
         return f"k_bb_row<{DT_NAME[dt]}, {D}> + k_bb_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32
