@@ -257,3 +257,28 @@ def test_nograd_descent_fused_wrapper_matches_eager(cuda):
     out = [en.descend(mf, z0, xe, steps, 0.1, create_graph=False, wrapper=w, noises=noises).detach()
            for w in ("fused", "eager")]
     assert float((out[0] - out[1]).abs().max()) <= 1e-5 * float(out[1].abs().max())
+
+
+def test_wrapper_functions_under_torch_compile(cuda):
+    """The reference compiles its wrapper functions (energy.py:249-261); the fused ones trace as opaque nodes under
+    torch.compile (aot_eager, no Triton) and give the eager kernels' results, forward and first-order backward."""
+    _say("descent under torch.compile")
+    torch._dynamo.reset()
+    B, L, C = 3, 16, 64
+    z, noise, grad, sigma, alpha, active = _inputs(B, L, C, torch.float32, seed=31)
+    zc, nc, gc = z.to(cuda), noise.to(cuda), grad.to(cuda)
+    sc, ac, mc = sigma.to(cuda), alpha.to(cuda), active.to(cuda)
+
+    def microstep(zz, gg):
+        v = descent.noisy_point(zz, nc, sc)
+        return descent.step_and_project(v, gg, ac, zz, mc)
+
+    compiled = torch.compile(microstep, backend="aot_eager", fullgraph=True)
+    w = torch.randn(z.shape, generator=torch.Generator().manual_seed(32)).to(cuda)
+    outs = []
+    for fn in (microstep, compiled):
+        zz, gg = zc.clone().requires_grad_(True), gc.clone().requires_grad_(True)
+        out = fn(zz, gg)
+        outs.append((out.detach(), *torch.autograd.grad((out * w).sum(), (zz, gg))))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
