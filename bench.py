@@ -332,8 +332,10 @@ def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
 
     B, L, V = 384, 81, 11
     dev = torch.device("cuda", 0)
-    # the fused 2D RoPE split/merge, as the reference's Sudoku recipe sets it (config/train/sudoku.yaml:11)
-    cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused", rope_impl="fused")
+    # the fused 2D RoPE split/merge, as the reference's Sudoku recipe sets it (config/train/sudoku.yaml:11), and the
+    # blocks' rms_norm / SwiGLU activation as fused kernels (the reference fuses that pointwise work by compiling dE/dz
+    # with inductor, models/energy.py:352-384)
+    cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused", rope_impl="fused", block_impl="fused")
     model, dec = en.build(cfg, dev)
     g = torch.Generator("cpu").manual_seed(0)
     x = torch.randint(0, V, (B, L), generator=g).to(dev)
@@ -355,7 +357,8 @@ def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
     ms = e0.elapsed_time(e1) / steps
     out = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 2), "loss": round(float(loss), 4),
            "config": "B=384 L=81 hidden=512 heads=8x64 layers=2 SwiGLU x4, 16 create_graph descent steps, bf16; 2D RoPE "
-                     "by the fused split/merge (the reference's Sudoku recipe); CPU: the broadcast RoPE",
+                     "by the fused split/merge (the reference's Sudoku recipe), rms_norm and SwiGLU activation by the "
+                     "fused block kernels; CPU: the same step eager (broadcast RoPE, eager block)",
            "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 2**30, 1)}
     if cpu_sample_b > 0:
         cores = len(os.sched_getaffinity(0))
@@ -386,7 +389,7 @@ def ebr_infer(cpu_sample_n: int):
 
     N, S, L, V, STEPS = 256, 20, 100, 3, 64
     dev = torch.device("cuda", 0)
-    cfg = en.EnergyConfig(grid=(10, 10), vocab_size=V)
+    cfg = en.EnergyConfig(grid=(10, 10), vocab_size=V, block_impl="fused")
     model, _ = en.build(cfg, dev)
     for p in model.parameters():
         p.requires_grad_(False)
@@ -399,7 +402,8 @@ def ebr_infer(cpu_sample_n: int):
     best, e = en.infer(model, x, z0, S, steps=STEPS)
     torch.cuda.synchronize()
     sec = time.perf_counter() - t
-    out = {"seconds": round(sec, 3), "config": "5120 x L=100, 64 descent steps (fwd+bwd), bf16, argmin over 20 samples"}
+    out = {"seconds": round(sec, 3), "config": "5120 x L=100, 64 descent steps (fwd+bwd), bf16, argmin over 20 samples; "
+           "rms_norm and SwiGLU activation by the fused block kernels; CPU: eager"}
     if cpu_sample_n > 0:
         torch.set_num_threads(len(os.sched_getaffinity(0)))
         ccfg = en.EnergyConfig(grid=(10, 10), vocab_size=V, attn_backend="math", attn_nograd_backend="math")
@@ -575,7 +579,8 @@ def descent_bench(reps: int, cpu: bool, train_steps: int) -> dict:
                                "sample": f"the CPU restatement (oracle.descent_ref forward + autograd VJPs) on batch "
                                f"{bs} of {B}, scaled linearly"}
     if train_steps > 0:
-        cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused", rope_impl="fused")
+        cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused", rope_impl="fused",
+                              block_impl="fused")
         model, dec = en.build(cfg, dev)
         gc = torch.Generator("cpu").manual_seed(0)
         x = torch.randint(0, 11, (B, L), generator=gc).to(dev)

@@ -1,5 +1,5 @@
-"""ctypes binding of ``libebr_attn.so`` (declared in ``include/ebr_attn.h``, ``include/ebr_rope.h`` and
-``include/ebr_descent.h``).
+"""ctypes binding of ``libebr_attn.so`` (declared in ``include/ebr_attn.h``, ``include/ebr_rope.h``,
+``include/ebr_descent.h`` and ``include/ebr_block.h``).
 
 The library is built in-tree by ``ebr_amd.build`` into ``ebr_amd/_lib/``. Loading needs only the HIP runtime, so the
 symbols can be checked on a machine without a GPU; every compute entry point needs a gfx950 device.
@@ -23,7 +23,7 @@ _P = ctypes.c_void_p
 _I64P = ctypes.POINTER(ctypes.c_int64)
 _F32P = ctypes.c_void_p  # fp32 device pointers are passed as raw addresses
 
-# name -> (restype, argtypes); mirrors include/ebr_attn.h, include/ebr_rope.h and include/ebr_descent.h
+# name -> (restype, argtypes); mirrors include/ebr_*.h
 SIGNATURES = {
     "ebr_attn_fwd": (
         ctypes.c_int,
@@ -70,6 +70,13 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int] * 2 + [ctypes.c_int64, ctypes.c_float] + [_P, _P, _F32P, _P, _F32P, _P, _P, _P, _P, _P],
     ),
+    # include/ebr_block.h
+    "ebr_block_rmsnorm": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_float] + [_P] * 3),
+    "ebr_block_rmsnorm_bwd": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_float] + [_P] * 4),
+    "ebr_block_rmsnorm_bwd2": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_float] + [_P] * 6),
+    "ebr_block_swiglu": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int] + [_P] * 3),
+    "ebr_block_swiglu_bwd": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int] + [_P] * 4),
+    "ebr_block_swiglu_bwd2": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int] + [_P] * 6),
     "ebr_attn_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ebr_attn_abi_version": (ctypes.c_int, []),
     "ebr_attn_arch": (ctypes.c_char_p, []),

@@ -19,7 +19,7 @@ OUT_DIR = PKG / "_lib"
 LIB_NAME = "libebr_attn.so"
 ARCH = "gfx950"
 
-SOURCES = [CSRC / "ebr_attn.hip", CSRC / "ebr_rope.hip", CSRC / "ebr_descent.hip"]
+SOURCES = [CSRC / "ebr_attn.hip", CSRC / "ebr_rope.hip", CSRC / "ebr_descent.hip", CSRC / "ebr_block.hip"]
 HEADERS = [
     CSRC / "attn_tiles.hpp",
     CSRC / "attn_resident.hpp",
@@ -27,6 +27,8 @@ HEADERS = [
     ROOT / "include" / "ebr_attn.h",
     ROOT / "include" / "ebr_rope.h",
     ROOT / "include" / "ebr_descent.h",
+    ROOT / "include" / "ebr_block.h",
+    CSRC / "attn_f64.hpp",
 ]
 
 

@@ -45,6 +45,7 @@ class EnergyConfig:
     attn_nograd_backend: str = "fused"
     rope: bool = True
     rope_impl: str = "broadcast"  # "fused": the HIP RoPE split/merge (RotaryTable2D), reference rope_impl
+    block_impl: str = "eager"  # "fused": rms_norm and the SwiGLU activation as HIP kernels (ebr_amd.block)
 
 
 class ScalarEnergy(nn.Module):

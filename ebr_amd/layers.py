@@ -65,13 +65,23 @@ def swiglu_intermediate(hidden_size: int, expansion: float) -> int:
 
 
 class SwiGLU(nn.Module):
-    def __init__(self, hidden_size: int, expansion: float) -> None:
+    """down(silu(gate) * up) with gate, up the halves of one projection; ``impl="fused"`` runs the activation (and its
+    first and second derivatives) as one HIP kernel each (``ebr_amd.block.swiglu``)."""
+
+    def __init__(self, hidden_size: int, expansion: float, impl: str = "eager") -> None:
         super().__init__()
+        if impl not in ("eager", "fused"):
+            raise ValueError(f"SwiGLU impl must be 'eager' or 'fused', got {impl!r}")
         inter = swiglu_intermediate(hidden_size, expansion)
         self.gate_up_proj = CastedLinear(hidden_size, 2 * inter, bias=False)
         self.down_proj = CastedLinear(inter, hidden_size, bias=False)
+        self.impl = impl
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.impl == "fused":
+            from ebr_amd import block
+
+            return self.down_proj(block.swiglu(self.gate_up_proj(x)))
         gate, up = self.gate_up_proj(x).chunk(2, dim=-1)
         return self.down_proj(F.silu(gate) * up)
 

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
     out = subprocess.run(["nm", "-D", "--defined-only", str(_capi.LIB_PATH)], capture_output=True, text=True).stdout
-    exported = set(re.findall(r"\b(ebr_(?:attn|rope|descent)_\w+)\b", out))
+    exported = set(re.findall(r"\b(ebr_(?:attn|rope|descent|block)_\w+)\b", out))
     assert exported == set(_declared())
 
 

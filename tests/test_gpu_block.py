@@ -1,0 +1,108 @@
+"""GPU parity of the fused energy-block kernels (``ebr_fused::block_*`` through the C ABI): rms_norm and the SwiGLU
+activation, forward, backward and backward-of-backward, against torch autograd of the eager formulas
+(``ebr_amd.layers.rms_norm``, ``F.silu(gate) * up``), plus fp64 gradcheck / gradgradcheck on the GPU and the energy
+network's graded training step with the fused block against the eager one.
+
+Bars: fp64 1e-10 (the second derivatives cancel terms of order 1, so their rounding differs at ~1e-12) and fp32 1e-5
+relative (max|a - ref| / max|ref|); bf16 / fp16 2e-2 (the kernels round each output once where eager chains several
+rounded kernels).
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from ebr_amd import block
+from ebr_amd import energy as en
+from ebr_amd import layers
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-5
+TOL = {torch.float64: 1e-10, torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _rel(a, r):
+    a, r = a.detach().double().cpu(), r.detach().double().cpu()
+    return float((a - r).abs().max() / r.abs().max().clamp_min(1e-30))
+
+
+def _eager_swiglu(gu):
+    g, u = gu.chunk(2, dim=-1)
+    return F.silu(g) * u
+
+
+def _three_orders(fn, x, seed):
+    """y, dL/dx (with create_graph) and d/dx <c, dL/dx> for L = <w, fn(x)>, plus the gradient w.r.t. w."""
+    g = torch.Generator().manual_seed(seed)
+    x = x.detach().clone().requires_grad_(True)
+    y = fn(x)
+    w = torch.randn(y.shape, generator=g).to(y).requires_grad_(True)
+    c = torch.randn(x.shape, generator=g).to(x)
+    (dx,) = torch.autograd.grad((y * w).sum(), x, create_graph=True)
+    gx, gw = torch.autograd.grad((dx * c).sum(), (x, w))
+    return y.detach(), dx.detach(), gx, gw
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(3, 9, 64), (2, 81, 512), (5, 7, 13), (2, 1, 3)])
+def test_rms_norm_three_orders(cuda, dtype, shape):
+    _say(f"rms_norm {shape} {dtype}")
+    x = (torch.randn(shape, generator=torch.Generator().manual_seed(1)) * 1.5).to(cuda, dtype)
+    got = _three_orders(lambda t: block.rms_norm(t, EPS), x, seed=2)
+    if dtype == torch.float64:  # layers.rms_norm (as the reference's) computes in fp32; the kernel keeps fp64
+        ref = _three_orders(lambda t: t * torch.rsqrt(t.square().mean(-1, keepdim=True) + EPS), x, seed=2)
+    else:
+        ref = _three_orders(lambda t: layers.rms_norm(t, EPS), x, seed=2)
+    for name, a, r in zip(("y", "dx", "d2x", "dw"), got, ref):
+        assert _rel(a, r) <= TOL[dtype], (name, _rel(a, r))
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(3, 9, 128), (2, 81, 3072), (4, 6)])
+def test_swiglu_three_orders(cuda, dtype, shape):
+    _say(f"swiglu {shape} {dtype}")
+    x = (torch.randn(shape, generator=torch.Generator().manual_seed(3)) * 2).to(cuda, dtype)
+    got = _three_orders(block.swiglu, x, seed=4)
+    ref = _three_orders(_eager_swiglu, x, seed=4)
+    for name, a, r in zip(("y", "dx", "d2x", "dw"), got, ref):
+        assert _rel(a, r) <= TOL[dtype], (name, _rel(a, r))
+
+
+def test_fp64_gradcheck_and_gradgradcheck(cuda):
+    _say("block gradcheck")
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 3, 8, generator=g, dtype=torch.float64).to(cuda).requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda t: block.rms_norm(t, EPS), (x,))
+    assert torch.autograd.gradgradcheck(lambda t: block.rms_norm(t, EPS), (x,))
+    gu = torch.randn(2, 3, 10, generator=g, dtype=torch.float64).to(cuda).requires_grad_(True)
+    assert torch.autograd.gradcheck(block.swiglu, (gu,))
+    assert torch.autograd.gradgradcheck(block.swiglu, (gu,))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_train_step_fused_block_matches_eager(cuda, dtype):
+    """The graded training step (second order through both blocks) with the fused block equals the eager one."""
+    _say(f"train step fused block {dtype}")
+    models = []
+    for impl in ("fused", "eager"):
+        cfg = en.EnergyConfig(hidden_size=64, num_heads=4, grid=(4, 4), block_impl=impl)
+        models.append(en.build(cfg, cuda, seed=41))
+    g = torch.Generator("cpu").manual_seed(42)
+    B, L = 3, 16
+    x = torch.randint(0, 11, (B, L), generator=g).to(cuda)
+    z0 = torch.randn(B, L, 64, generator=g).to(cuda, dtype)
+    tg = torch.randint(0, 11, (B, L), generator=g).to(cuda)
+    losses = [float(en.train_step(m, d, x, z0, tg, steps=3)) for m, d in models]
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert abs(losses[0] - losses[1]) <= tol * max(1.0, abs(losses[1]))
+    gtol = 1e-4 if dtype == torch.float32 else 1e-1
+    (mf, _), (me, _) = models
+    for (n, pf), (_, pe) in zip(mf.named_parameters(), me.named_parameters()):
+        if pe.grad is not None:
+            err = float((pf.grad.float() - pe.grad.float()).abs().max() / pe.grad.float().abs().max().clamp_min(1e-12))
+            assert err <= gtol, (n, err)
