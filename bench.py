@@ -606,16 +606,118 @@ def descent_bench(reps: int, cpu: bool, train_steps: int) -> dict:
     return res
 
 
+def block_bench(reps: int) -> dict:
+    """The fused energy-block kernels (ebr_fused::block_*) at the training step's shapes: rms_norm over rows of 512
+    ([384 x 81] tokens) and the SwiGLU activation over rows of 2 x 1536, bf16. Each kernel's average time over ``reps``
+    back-to-back C-ABI launches on rotating inputs (HIP events on the launch stream) and the achieved GB/s of its
+    algorithmic bytes against the 8 TB/s peak; then the same three orders (value, gradient with ``create_graph``, its
+    gradient) of each function as eager torch autograd on the GPU, against the three fused kernels."""
+    import torch.nn.functional as F
+
+    from ebr_amd import block  # noqa: F401  (registers the ops)
+    from ebr_amd import layers
+
+    rows, C, inter, dt, eps = 384 * 81, 512, 1536, torch.bfloat16, layers.RMS_NORM_EPS
+    dev = torch.device("cuda", 0)
+    lib = _capi.load()
+    code = _capi.DTYPE_BF16
+    SN, SG, SA = rows * C * 2, rows * 2 * inter * 2, rows * inter * 2  # norm row, [gate | up] row, activation row
+    nsets = max(2, -(-MALL_FLUSH_BYTES // (2 * SG)))
+    g = torch.Generator(device=dev).manual_seed(9)
+    mk = lambda n: [torch.randn((rows, n), generator=g, device=dev).to(dt) for _ in range(nsets)]  # noqa: E731
+    xs, dys, cs = mk(C), mk(C), mk(C)
+    gus, das, cgs = mk(2 * inter), mk(inter), mk(2 * inter)
+    on, on2 = torch.empty_like(xs[0]), torch.empty_like(xs[0])
+    og, og2 = torch.empty_like(gus[0]), torch.empty_like(das[0])
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: t.data_ptr()  # noqa: E731
+    calls = {
+        "rmsnorm": (2 * SN, lambda i: lib.ebr_block_rmsnorm(code, rows, C, eps, P(xs[i]), P(on), sp)),
+        "rmsnorm_bwd": (3 * SN, lambda i: lib.ebr_block_rmsnorm_bwd(code, rows, C, eps, P(xs[i]), P(dys[i]), P(on),
+                                                                   sp)),
+        "rmsnorm_bwd2": (5 * SN, lambda i: lib.ebr_block_rmsnorm_bwd2(code, rows, C, eps, P(xs[i]), P(dys[i]),
+                                                                     P(cs[i]), P(on), P(on2), sp)),
+        "swiglu": (SG + SA, lambda i: lib.ebr_block_swiglu(code, rows, inter, P(gus[i]), P(og2), sp)),
+        "swiglu_bwd": (2 * SG + SA, lambda i: lib.ebr_block_swiglu_bwd(code, rows, inter, P(gus[i]), P(das[i]),
+                                                                      P(og), sp)),
+        "swiglu_bwd2": (3 * SG + 2 * SA, lambda i: lib.ebr_block_swiglu_bwd2(code, rows, inter, P(gus[i]), P(das[i]),
+                                                                            P(cgs[i]), P(og), P(og2), sp)),
+    }  # fmt: skip
+    res = {"shape": f"rms_norm [{rows}, {C}], SwiGLU [{rows}, 2 x {inter}] bf16"}
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(n):
+            fn(i % nsets)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    for name, (nbytes, fn) in calls.items():
+        for i in range(3):
+            _capi.check(fn(i % nsets), name)
+        us = timed(fn, reps)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "gbs": round(gbs, 1),
+                     "frac_hbm": round(gbs / roofline.PEAK_HBM_GBS, 4)}
+
+    def three_orders(f, ins, douts, cots):
+        def run(i):
+            x = ins[i].detach().requires_grad_(True)
+            y = f(x)
+            (dx,) = torch.autograd.grad(y, x, douts[i], create_graph=True)
+            return torch.autograd.grad(dx, x, cots[i])
+
+        return run
+
+    def eager_swiglu(gu):
+        a, b = gu.chunk(2, dim=-1)
+        return F.silu(a) * b
+
+    for label, eager, fused, ins, douts, cots, keys in (
+        ("rmsnorm", lambda x: layers.rms_norm(x, eps), lambda x: block.rms_norm(x, eps), xs, dys, cs,
+         ("rmsnorm", "rmsnorm_bwd", "rmsnorm_bwd2")),
+        ("swiglu", eager_swiglu, block.swiglu, gus, das, cgs, ("swiglu", "swiglu_bwd", "swiglu_bwd2")),
+    ):  # fmt: skip
+        fe, ff = three_orders(eager, ins, douts, cots), three_orders(fused, ins, douts, cots)
+        for i in range(2):
+            fe(i)
+            ff(i)
+        n = max(3, reps // 4)
+        e_us, f_us = timed(fe, n), timed(ff, n)
+        res[f"{label}_three_orders"] = {"kernels_us": round(sum(res[k]["us"] for k in keys), 1),
+                                        "fused_autograd_us": round(f_us, 1), "eager_autograd_us": round(e_us, 1),
+                                        "speedup_vs_eager": round(e_us / f_us, 2)}
+    return res
+
+
+def block_target(reps: int = 20) -> None:
+    """The energy-block leg alone, for ``rocprofv3``: the 256 MiB calibration copy, then ``block_bench``."""
+    dev = torch.device("cuda", 0)
+    src = torch.empty(64 << 20, device=dev, dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    print(json.dumps(block_bench(reps)), flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--no-ebr", action="store_true", help="skip the EBR training-step measurement (config 3)")
     ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE split/merge measurement")
     ap.add_argument("--no-descent", action="store_true", help="skip the fused descent-wrapper measurement")
     ap.add_argument("--no-multi", action="store_true", help="skip the multi-solution (D = 128) attention shapes")
+    ap.add_argument("--no-block", action="store_true", help="skip the fused energy-block (rms_norm, SwiGLU) leg")
     ap.add_argument("--ebr-infer", action="store_true", help="also run the inference descent (config 4)")
     ap.add_argument("--ebr-steps", type=int, default=3)
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
     ap.add_argument("--descent-target", action="store_true", help="run only the descent-wrapper leg (for rocprofv3)")
+    ap.add_argument("--block-target", action="store_true", help="run only the energy-block leg (for rocprofv3)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
@@ -643,6 +745,9 @@ def main() -> int:
 
     if args.descent_target:
         descent_target()
+        return 0
+    if args.block_target:
+        block_target()
         return 0
     cfg = CONFIGS[args.config]
     if args.pmc_target:
@@ -747,6 +852,10 @@ def main() -> int:
         log("fused descent wrapper")
         out["descent"] = descent_bench(20, not args.no_cpu, 0 if args.no_ebr else 2)
         log(f"descent: {out['descent']}")
+    if not args.no_block:
+        log("fused energy block")
+        out["block"] = block_bench(20)
+        log(f"block: {out['block']}")
     if not args.no_ebr:
         log("EBR training step (config 3)")
         out["ebr_train"] = ebr_train(args.ebr_steps, 1, 0 if args.no_cpu else 8)

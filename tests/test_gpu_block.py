@@ -49,7 +49,11 @@ def _three_orders(fn, x, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(3, 9, 64), (2, 81, 512), (5, 7, 13), (2, 1, 3)])
+# widths cover the register-resident vector kernels (1 to 4 vectors per lane, a partial last vector, row counts that
+# leave the last wave short) and the streaming fallback (odd widths, rows beyond 4 vectors per lane)
+@pytest.mark.parametrize(
+    "shape", [(3, 9, 64), (2, 81, 512), (5, 7, 13), (2, 1, 3), (3, 7, 1024), (1, 5, 1544), (2, 3, 2056), (1, 9, 520)]
+)
 def test_rms_norm_three_orders(cuda, dtype, shape):
     _say(f"rms_norm {shape} {dtype}")
     x = (torch.randn(shape, generator=torch.Generator().manual_seed(1)) * 1.5).to(cuda, dtype)
@@ -63,7 +67,9 @@ def test_rms_norm_three_orders(cuda, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(3, 9, 128), (2, 81, 3072), (4, 6)])
+# I = 64 and 1536: vector kernel; I = 3: element kernel; I = 12: vector kernel for fp32 / fp64, element kernel for
+# 16-bit (not a multiple of 8)
+@pytest.mark.parametrize("shape", [(3, 9, 128), (2, 81, 3072), (4, 6), (5, 7, 24)])
 def test_swiglu_three_orders(cuda, dtype, shape):
     _say(f"swiglu {shape} {dtype}")
     x = (torch.randn(shape, generator=torch.Generator().manual_seed(3)) * 2).to(cuda, dtype)
@@ -71,6 +77,37 @@ def test_swiglu_three_orders(cuda, dtype, shape):
     ref = _three_orders(_eager_swiglu, x, seed=4)
     for name, a, r in zip(("y", "dx", "d2x", "dw"), got, ref):
         assert _rel(a, r) <= TOL[dtype], (name, _rel(a, r))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_misaligned_rows_take_the_element_kernels(cuda, dtype):
+    """Tensors that start 2 or 4 bytes past a 16-byte boundary (contiguous, so no copy is made) give the same results
+    as aligned copies of the same values."""
+    _say(f"block misaligned {dtype}")
+    g = torch.Generator().manual_seed(8)
+    for width, fn in ((512, lambda t: block.rms_norm(t, EPS)), (256, block.swiglu)):
+        n = 6 * width
+        buf = torch.randn(n + 1, generator=g).to(cuda, dtype)
+        x = buf[1:].view(6, width)
+        assert x.is_contiguous() and x.data_ptr() % 16 != 0
+        got = _three_orders(fn, x, seed=9)
+        ref = _three_orders(fn, x.clone(), seed=9)
+        for name, a, r in zip(("y", "dx", "d2x", "dw"), got, ref):
+            assert _rel(a, r) <= TOL[dtype], (width, name, _rel(a, r))
+
+
+def test_swiglu_64bit_offsets(cuda):
+    """A gate / up tensor of more than 2^31 elements: the vector kernel's 64-bit index variant."""
+    _say("swiglu 64-bit offsets")
+    rows, inter = (1 << 20) + 1, 1024
+    gen = torch.Generator(cuda).manual_seed(3)
+    gu = torch.empty(rows, 2 * inter, device=cuda, dtype=torch.bfloat16).normal_(generator=gen)
+    assert gu.numel() >= (1 << 31)
+    y = block.swiglu(gu)
+    ref = _eager_swiglu(gu)
+    del gu
+    assert _rel(y[-4:], ref[-4:]) <= TOL[torch.bfloat16]  # rows past the 2^31st element
+    assert _rel(y, ref) <= TOL[torch.bfloat16]
 
 
 def test_fp64_gradcheck_and_gradgradcheck(cuda):
