@@ -30,7 +30,15 @@ import torch.nn.functional as F
 from torch import nn
 
 from ebr_amd.attention import EnergyReasoningBlock, second_order_window
-from ebr_amd.layers import RMS_NORM_EPS, CastedLinear, RotaryEmbedding2D, RotaryTable2D, rms_norm, trunc_normal_init_
+from ebr_amd.layers import (
+    RMS_NORM_EPS,
+    CastedLinear,
+    RotaryEmbedding2D,
+    RotaryTable2D,
+    check_linear_impl,
+    rms_norm,
+    trunc_normal_init_,
+)
 
 
 @dataclass
@@ -46,6 +54,7 @@ class EnergyConfig:
     rope: bool = True
     rope_impl: str = "broadcast"  # "fused": the HIP RoPE split/merge (RotaryTable2D), reference rope_impl
     block_impl: str = "eager"  # "fused": rms_norm and the SwiGLU activation as HIP kernels (ebr_amd.block)
+    linear_impl: str = "eager"  # "splitk": projection weight gradients as split-K GEMMs (ebr_amd.linear)
 
 
 class ScalarEnergy(nn.Module):
@@ -299,6 +308,10 @@ def build(cfg: EnergyConfig, device: torch.device, seed: int = 0):
     torch.manual_seed(seed)
     model = ScalarEnergy(cfg).to(device)
     decoder = Decoder(cfg).to(device)
+    impl = check_linear_impl(cfg.linear_impl)
+    for m in (*model.modules(), *decoder.modules()):
+        if isinstance(m, CastedLinear):
+            m.impl = impl
     return model, decoder
 
 

@@ -46,17 +46,29 @@ def rms_norm(x: torch.Tensor, variance_epsilon: float) -> torch.Tensor:
 
 
 class CastedLinear(nn.Module):
-    """y = x W^T (+ b) with fp32 parameters cast to x.dtype at every call."""
+    """y = x W^T (+ b) with fp32 parameters cast to x.dtype at every call. ``impl="splitk"`` takes the weight
+    gradients as split-K GEMMs with fp32 partials (``ebr_amd.linear``); the values are those of ``F.linear``."""
 
-    def __init__(self, in_features: int, out_features: int, bias: bool) -> None:
+    def __init__(self, in_features: int, out_features: int, bias: bool, impl: str = "eager") -> None:
         super().__init__()
         w = torch.empty(out_features, in_features)
         self.weight = nn.Parameter(trunc_normal_init_(w, std=in_features**-0.5))
         self.bias = nn.Parameter(torch.zeros(out_features)) if bias else None
+        self.impl = check_linear_impl(impl)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         b = None if self.bias is None else self.bias.to(x.dtype)
+        if self.impl == "splitk":
+            from ebr_amd import linear
+
+            return linear.linear(x, self.weight.to(x.dtype), b)
         return F.linear(x, self.weight.to(x.dtype), b)
+
+
+def check_linear_impl(impl: str) -> str:
+    if impl not in ("eager", "splitk"):
+        raise ValueError(f"linear impl must be 'eager' or 'splitk', got {impl!r}")
+    return impl
 
 
 def swiglu_intermediate(hidden_size: int, expansion: float) -> int:
@@ -172,6 +184,7 @@ __all__ = [
     "quarter_swap",
     "SwiGLU",
     "apply_rope",
+    "check_linear_impl",
     "rms_norm",
     "rotate_half",
     "swiglu_intermediate",
