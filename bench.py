@@ -602,6 +602,8 @@ def descent_bench(reps: int, cpu: bool, train_steps: int) -> dict:
             model.zero_grad(set_to_none=True)
             dec.zero_grad(set_to_none=True)
             torch.cuda.synchronize()
+            gc.collect()
+            gc.freeze()  # as in ebr_train: no full collection inside the timed steps
             t0 = time.perf_counter()
             for _ in range(train_steps):
                 run()
@@ -609,6 +611,7 @@ def descent_bench(reps: int, cpu: bool, train_steps: int) -> dict:
                 dec.zero_grad(set_to_none=True)
             torch.cuda.synchronize()
             steps[wrapper] = round(train_steps / (time.perf_counter() - t0), 3)
+            gc.unfreeze()
         res["train_step_steps_per_s"] = steps
         res["train_step_config"] = ("config 3's network and batch with the reference microstep (rms_norm + noise, "
                                     "sphere projection, per-row sigma / alpha), 16 graded steps")
@@ -859,7 +862,7 @@ def main() -> int:
         log(f"multi-solution: {out['multi_solution']}")
     if not args.no_descent:
         log("fused descent wrapper")
-        out["descent"] = descent_bench(20, not args.no_cpu, 0 if args.no_ebr else 2)
+        out["descent"] = descent_bench(20, not args.no_cpu, 0 if args.no_ebr else 3)
         log(f"descent: {out['descent']}")
     if not args.no_block:
         log("fused energy block")
