@@ -591,10 +591,10 @@ def descent_bench(reps: int, cpu: bool, train_steps: int) -> dict:
         cfg = en.EnergyConfig(attn_backend="fused", attn_nograd_backend="fused", rope_impl="fused",
                               block_impl="fused", linear_impl="splitk")
         model, dec = en.build(cfg, dev)
-        gc = torch.Generator("cpu").manual_seed(0)
-        x = torch.randint(0, 11, (B, L), generator=gc).to(dev)
-        z0 = torch.randn(B, L, C, generator=gc).to(dev, dt)
-        tg = torch.randint(0, 11, (B, L), generator=gc).to(dev)
+        gen = torch.Generator("cpu").manual_seed(0)
+        x = torch.randint(0, 11, (B, L), generator=gen).to(dev)
+        z0 = torch.randn(B, L, C, generator=gen).to(dev, dt)
+        tg = torch.randint(0, 11, (B, L), generator=gen).to(dev)
         steps = {}
         for wrapper in ("fused", "eager"):
             run = lambda: en.train_step(model, dec, x, z0, tg, alpha=alpha, wrapper=wrapper, sigma=sigma)  # noqa

@@ -38,7 +38,22 @@ def _c(t: Tensor) -> Tensor:
 
 
 def _rows(x: Tensor) -> Tuple[int, int]:
-    return x.numel() // x.shape[-1], x.shape[-1]
+    if x.dim() < 1:
+        raise ValueError(f"fused block: expected a tensor with a last dim, got {tuple(x.shape)}")
+    return x.numel() // max(1, x.shape[-1]), x.shape[-1]
+
+
+def _like(t: Tensor, shape, ref: Tensor, name: str) -> None:
+    """An operand the kernels index by ``ref``'s rows (the C ABI takes only ``ref``'s sizes)."""
+    if tuple(t.shape) != tuple(shape) or t.device != ref.device:
+        raise ValueError(f"fused block: {name} is {tuple(t.shape)} on {t.device}, expected {tuple(shape)} on "
+                         f"{ref.device}")
+
+
+def _half(gu: Tensor) -> int:
+    if gu.dim() < 1 or gu.shape[-1] % 2:
+        raise ValueError(f"fused block: swiglu needs an even last dim, got {tuple(gu.shape)}")
+    return gu.shape[-1] // 2
 
 
 # ---------------------------------------------------------------------------------------------------------------------
@@ -52,6 +67,8 @@ def rmsnorm_op(x: Tensor, eps: float) -> Tensor:
     x = _c(x)
     rows, C = _rows(x)
     y = torch.empty_like(x)
+    if y.numel() == 0:
+        return y
     with torch.cuda.device(x.device):
         rc = lib.ebr_block_rmsnorm(_code(x), rows, C, eps, x.data_ptr(), y.data_ptr(), _stream(x))
     _capi.check(rc, "ebr_block_rmsnorm")
@@ -66,9 +83,12 @@ def _(x, eps):
 @torch.library.custom_op("ebr_fused::block_rmsnorm_bwd", mutates_args=(), device_types="cuda")
 def rmsnorm_bwd_op(x: Tensor, dy: Tensor, eps: float) -> Tensor:
     lib = hip_library()
+    _like(dy, x.shape, x, "dy")
     x, dy = _c(x), _c(dy.to(x.dtype))
     rows, C = _rows(x)
     dx = torch.empty_like(x)
+    if dx.numel() == 0:
+        return dx
     with torch.cuda.device(x.device):
         rc = lib.ebr_block_rmsnorm_bwd(_code(x), rows, C, eps, x.data_ptr(), dy.data_ptr(), dx.data_ptr(), _stream(x))
     _capi.check(rc, "ebr_block_rmsnorm_bwd")
@@ -83,9 +103,13 @@ def _(x, dy, eps):
 @torch.library.custom_op("ebr_fused::block_rmsnorm_bwd2", mutates_args=(), device_types="cuda")
 def rmsnorm_bwd2_op(x: Tensor, dy: Tensor, c: Tensor, eps: float) -> Tuple[Tensor, Tensor]:
     lib = hip_library()
+    _like(dy, x.shape, x, "dy")
+    _like(c, x.shape, x, "c")
     x, dy, c = _c(x), _c(dy.to(x.dtype)), _c(c.to(x.dtype))
     rows, C = _rows(x)
     gx, gdy = torch.empty_like(x), torch.empty_like(x)
+    if gx.numel() == 0:
+        return gx, gdy
     with torch.cuda.device(x.device):
         rc = lib.ebr_block_rmsnorm_bwd2(
             _code(x), rows, C, eps, x.data_ptr(), dy.data_ptr(), c.data_ptr(), gx.data_ptr(), gdy.data_ptr(),
@@ -145,9 +169,12 @@ class _RmsNorm(torch.autograd.Function):
 @torch.library.custom_op("ebr_fused::block_swiglu", mutates_args=(), device_types="cuda")
 def swiglu_op(gu: Tensor) -> Tensor:
     lib = hip_library()
+    _half(gu)
     gu = _c(gu)
     rows, two_i = _rows(gu)
     y = gu.new_empty((*gu.shape[:-1], two_i // 2))
+    if y.numel() == 0:
+        return y
     with torch.cuda.device(gu.device):
         rc = lib.ebr_block_swiglu(_code(gu), rows, two_i // 2, gu.data_ptr(), y.data_ptr(), _stream(gu))
     _capi.check(rc, "ebr_block_swiglu")
@@ -162,9 +189,12 @@ def _(gu):
 @torch.library.custom_op("ebr_fused::block_swiglu_bwd", mutates_args=(), device_types="cuda")
 def swiglu_bwd_op(gu: Tensor, dy: Tensor) -> Tensor:
     lib = hip_library()
+    _like(dy, (*gu.shape[:-1], _half(gu)), gu, "dy")
     gu, dy = _c(gu), _c(dy.to(gu.dtype))
     rows, two_i = _rows(gu)
     dgu = torch.empty_like(gu)
+    if dgu.numel() == 0:
+        return dgu
     with torch.cuda.device(gu.device):
         rc = lib.ebr_block_swiglu_bwd(_code(gu), rows, two_i // 2, gu.data_ptr(), dy.data_ptr(), dgu.data_ptr(),
                                       _stream(gu))
@@ -180,9 +210,13 @@ def _(gu, dy):
 @torch.library.custom_op("ebr_fused::block_swiglu_bwd2", mutates_args=(), device_types="cuda")
 def swiglu_bwd2_op(gu: Tensor, dy: Tensor, c: Tensor) -> Tuple[Tensor, Tensor]:
     lib = hip_library()
+    _like(dy, (*gu.shape[:-1], _half(gu)), gu, "dy")
+    _like(c, gu.shape, gu, "c")
     gu, dy, c = _c(gu), _c(dy.to(gu.dtype)), _c(c.to(gu.dtype))
     rows, two_i = _rows(gu)
     ggu, gdy = torch.empty_like(gu), torch.empty_like(dy)
+    if ggu.numel() == 0:
+        return ggu, gdy
     with torch.cuda.device(gu.device):
         rc = lib.ebr_block_swiglu_bwd2(
             _code(gu), rows, two_i // 2, gu.data_ptr(), dy.data_ptr(), c.data_ptr(), ggu.data_ptr(), gdy.data_ptr(),
@@ -237,8 +271,7 @@ def rms_norm(x: Tensor, eps: float) -> Tensor:
 
 def swiglu(gate_up: Tensor) -> Tensor:
     """silu(gate) * up of the two halves of the last dim, differentiable twice."""
-    if gate_up.shape[-1] % 2:
-        raise ValueError(f"fused block: swiglu needs an even last dim, got {gate_up.shape[-1]}")
+    _half(gate_up)
     return _SwiGLU.apply(gate_up)
 
 

@@ -62,6 +62,21 @@ def _per_row(x: Scalar, rows: int, dtype: torch.dtype, device, name: str) -> Ten
     return x.reshape(-1).expand(rows).to(device=device, dtype=torch.float32).contiguous()
 
 
+def _like(t: Tensor, ref: Tensor, name: str) -> None:
+    """An operand the kernels index like ``ref`` (the C ABI takes only ``ref``'s sizes)."""
+    if t.shape != ref.shape or t.device != ref.device:
+        raise ValueError(f"descent wrapper: {name} is {tuple(t.shape)} on {t.device}, expected {tuple(ref.shape)} on "
+                         f"{ref.device}")
+
+
+def _row_vec(t: Tensor, rows: int, dtype: torch.dtype, ref: Tensor, name: str) -> Tensor:
+    """A per-row operand of the ops: ``rows`` elements of ``dtype`` on ``ref``'s device."""
+    if t.numel() != rows or t.dtype != dtype or t.device != ref.device:
+        raise ValueError(f"descent wrapper: {name} must be {rows} {dtype} values on {ref.device}, got "
+                         f"{tuple(t.shape)} {t.dtype} on {t.device}")
+    return _contig(t.reshape(rows))
+
+
 def _mask(active: Optional[Tensor], rows: int, device) -> Optional[Tensor]:
     if active is None:
         return None
@@ -80,11 +95,17 @@ def noisy_point_op(z: Tensor, noise: Optional[Tensor], sigma: Optional[Tensor], 
     """v = rms_norm(z) (+ noise) (+ round(noise * sigma[b])); ``sigma`` fp32 [B] or None."""
     lib = hip_library()
     code = _dtype_code(z)
+    _check_board(z, "z")
     z = _contig(z)
     B, L, C = z.shape
     if noise is not None:
+        _like(noise, z, "noise")
         noise = _contig(noise.to(z.dtype))
+    if sigma is not None:
+        sigma = _row_vec(sigma, B, torch.float32, z, "sigma")
     v = torch.empty_like(z)
+    if v.numel() == 0:
+        return v
     with torch.cuda.device(z.device):
         rc = lib.ebr_descent_noisy_point(code, B, L, C, eps, z.data_ptr(), _ptr(noise), _ptr(sigma), v.data_ptr(),
                                          _stream(z))
@@ -101,9 +122,13 @@ def _(z, noise, sigma, eps):
 def noisy_point_bwd_op(z: Tensor, dv: Tensor, eps: float) -> Tensor:
     lib = hip_library()
     code = _dtype_code(z)
+    _check_board(z, "z")
+    _like(dv, z, "dv")
     z, dv = _contig(z), _contig(dv.to(z.dtype))
     B, L, C = z.shape
     dz = torch.empty_like(z)
+    if dz.numel() == 0:
+        return dz
     with torch.cuda.device(z.device):
         rc = lib.ebr_descent_noisy_point_bwd(code, B, L, C, eps, z.data_ptr(), dv.data_ptr(), dz.data_ptr(), _stream(z))
     _capi.check(rc, "ebr_descent_noisy_point_bwd")
@@ -121,10 +146,19 @@ def step_project_op(v: Tensor, g: Tensor, alpha: Tensor, z: Optional[Tensor], ac
     """(where(active, sphere(v - round(alpha g)), z), rms [B] fp32); ``alpha`` fp32 [B], ``active`` uint8 [B]."""
     lib = hip_library()
     code = _dtype_code(v)
+    _check_board(v, "v")
+    _like(g, v, "g")
     v, g = _contig(v), _contig(g.to(v.dtype))
     B = v.shape[0]
+    if v.numel() == 0:
+        return torch.empty_like(v), v.new_zeros((B,), dtype=torch.float32)
     N = v.numel() // B
+    alpha = _row_vec(alpha, B, torch.float32, v, "alpha")
     if active is not None:
+        if z is None:
+            raise ValueError("descent wrapper: a row mask needs z (the rows it keeps)")
+        _like(z, v, "z")
+        active = _row_vec(active, B, torch.uint8, v, "active")
         z = _contig(z.to(v.dtype))
     out = torch.empty_like(v)
     rms = torch.empty((B,), device=v.device, dtype=torch.float32)
@@ -148,9 +182,19 @@ def step_project_bwd_op(v: Tensor, g: Tensor, alpha: Tensor, active: Optional[Te
     """(dv, dg, dz); dz is an empty tensor when ``active`` is None (every row moves, so it would be zero)."""
     lib = hip_library()
     code = _dtype_code(v)
+    _check_board(v, "v")
+    _like(g, v, "g")
+    _like(dout, v, "dout")
     v, g, dout = _contig(v), _contig(g.to(v.dtype)), _contig(dout.to(v.dtype))
     B = v.shape[0]
+    if v.numel() == 0:
+        dz = torch.empty_like(v) if active is not None else v.new_empty((0,))
+        return torch.empty_like(v), torch.empty_like(v), dz
     N = v.numel() // B
+    alpha = _row_vec(alpha, B, torch.float32, v, "alpha")
+    rms = _row_vec(rms, B, torch.float32, v, "rms")
+    if active is not None:
+        active = _row_vec(active, B, torch.uint8, v, "active")
     dv, dg = torch.empty_like(v), torch.empty_like(v)
     dz = torch.empty_like(v) if active is not None else v.new_empty((0,))
     with torch.cuda.device(v.device):

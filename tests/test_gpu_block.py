@@ -143,3 +143,25 @@ def test_train_step_fused_block_matches_eager(cuda, dtype):
         if pe.grad is not None:
             err = float((pf.grad.float() - pe.grad.float()).abs().max() / pe.grad.float().abs().max().clamp_min(1e-12))
             assert err <= gtol, (n, err)
+
+
+def test_ops_reject_mismatched_operands_and_take_empty_inputs(cuda):
+    """The C ABI takes only x's (or gu's) sizes, so every other operand is checked against them before a launch;
+    empty tensors return empty results without one."""
+    x = torch.randn(4, 64, device=cuda)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.block_rmsnorm_bwd(x, x[:3], EPS)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.block_rmsnorm_bwd2(x, x, x[:, :32], EPS)
+    gu = torch.randn(4, 64, device=cuda)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.block_swiglu_bwd(gu, gu)  # dy must have the half width
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.block_swiglu_bwd2(gu, gu[:, :32], gu[:2])
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.block_swiglu(torch.randn(4, 7, device=cuda))
+    e = torch.empty(0, 64, device=cuda)
+    assert block.rms_norm(e, EPS).shape == (0, 64) and block.swiglu(e).shape == (0, 32)
+    xe = e.clone().requires_grad_(True)
+    (dx,) = torch.autograd.grad(block.rms_norm(xe, EPS).sum(), xe, create_graph=True)
+    assert dx.shape == (0, 64)

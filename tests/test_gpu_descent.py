@@ -210,6 +210,32 @@ def test_c_abi_errors(cuda):
         descent.normalize(torch.zeros(2, 3, 8, device=cuda, dtype=torch.float64))
 
 
+def test_ops_reject_mismatched_operands_and_take_empty_inputs(cuda):
+    """The C ABI takes only the board's sizes, so every other operand of the raw ops is checked against them before a
+    launch; an empty batch returns empty results without one."""
+    z = torch.randn(2, 3, 8, device=cuda)
+    row = torch.ones(2, device=cuda)
+    ops = torch.ops.ebr_fused
+    with pytest.raises(ValueError):
+        ops.descent_noisy_point(z, z[:1], None, EPS)
+    with pytest.raises(ValueError):
+        ops.descent_noisy_point(z, z, torch.ones(3, device=cuda), EPS)  # sigma per row: 2 values
+    with pytest.raises(ValueError):
+        ops.descent_noisy_point_bwd(z, z[:, :2], EPS)
+    with pytest.raises(ValueError):
+        ops.descent_step_project(z, z, torch.ones(1, device=cuda), None, None, EPS)
+    with pytest.raises(ValueError):
+        ops.descent_step_project(z, z, row, z, torch.ones(2, device=cuda), EPS)  # the mask must be uint8
+    with pytest.raises(ValueError):
+        ops.descent_step_project(z, z, row, None, torch.ones(2, device=cuda, dtype=torch.uint8), EPS)
+    with pytest.raises(ValueError):
+        ops.descent_step_project_bwd(z, z, row, None, torch.ones(5, device=cuda), z, EPS)  # rms per row
+    e = torch.empty(0, 3, 8, device=cuda)
+    assert ops.descent_noisy_point(e, None, None, EPS).shape == e.shape
+    out, rms = ops.descent_step_project(e, e, torch.empty(0, device=cuda), None, None, EPS)
+    assert out.shape == e.shape and rms.shape == (0,)
+
+
 def _energy_models(cuda):
     """Two copies of one small energy network (fp32 parameters; activations follow the latent's dtype)."""
     cfg = en.EnergyConfig(hidden_size=64, num_heads=4, grid=(4, 4))
