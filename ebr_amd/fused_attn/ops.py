@@ -62,6 +62,18 @@ def _check(q: Tensor, k: Tensor, v: Tensor) -> None:
         )
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError(f"fused attention expects one dtype; got {q.dtype}, {k.dtype}, {v.dtype}")
+    if not (q.device == k.device == v.device):
+        raise ValueError(f"fused attention expects one device; got {q.device}, {k.device}, {v.device}")
+
+
+def _check_like(q: Tensor, **named: Tensor) -> None:
+    """o, dO and the cotangents are read as [B, H, N, D] and lse as [B, H, N] by q's sizes (the C ABI takes only
+    those), so a tensor of another shape or device is refused before any launch."""
+    for name, t in named.items():
+        want = q.shape[:-1] if name == "lse" else q.shape
+        if t.shape != want or t.device != q.device:
+            raise ValueError(f"fused attention: {name} is {tuple(t.shape)} on {t.device}, expected {tuple(want)} on "
+                             f"{q.device}")
 
 
 def _dtype_code(t: Tensor) -> int:
@@ -142,6 +154,7 @@ def attn_bwd(
     q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, do: Tensor, scale: float
 ) -> Tuple[Tensor, Tensor, Tensor]:
     _check(q, k, v)
+    _check_like(q, o=o, lse=lse, do=do)
     do = do.to(q.dtype)  # reference ops.py:84
     lib = hip_library()
     code = _dtype_code(q)
@@ -186,6 +199,7 @@ def attn_bwd_bwd(
 ) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     del dq  # part of the op contract; the kernels recompute dS tile by tile (reference reference.py:74)
     _check(q, k, v)
+    _check_like(q, o=o, lse=lse, do=do, gq=gq, gk=gk, gv=gv)
     lib = hip_library()
     code = _dtype_code(q)
     q, k, v = _rows(q), _rows(k), _rows(v)

@@ -173,6 +173,13 @@ def test_argument_errors():
     with pytest.raises(TypeError):
         ops._dtype_code(q.to(torch.int32))
     assert ops._dtype_code(q.double()) == 3  # fp64 has kernels of its own
+    ops._check_like(q, o=q, lse=q[..., 0], do=q)
+    with pytest.raises(ValueError):
+        ops._check_like(q, o=q[:, :1])  # o is read by q's sizes
+    with pytest.raises(ValueError):
+        ops._check_like(q, lse=q)  # lse is [B, H, N]
+    with pytest.raises(ValueError):
+        ops._check_like(q, gk=q[..., :4])
     assert ops.default_scale(q, None) == 8**-0.5 and ops.default_scale(q, 0.3) == 0.3
 
 

@@ -145,3 +145,19 @@ def test_energy_fused_rope_matches_broadcast(cuda):
     vf = en.descend(mf, z0, xe, 3, 0.1, create_graph=False).detach()
     vb = en.descend(mb, z0, xe, 3, 0.1, create_graph=False).detach()
     assert float((vf - vb).abs().max()) <= 1e-4 * float(vb.abs().max())
+
+
+def test_raw_ops_check_operands(cuda):
+    """The C ABI takes only the sizes of qkv (split) or dq (merge); the raw ops check every other operand first."""
+    cos = torch.zeros(9, 16, device=cuda)
+    qkv = torch.zeros(2, 9, 96, device=cuda, dtype=torch.bfloat16)
+    none = torch.zeros(0, device=cuda)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.rope_split(qkv, cos[:8], cos[:8], none, 2)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.rope_split(qkv, cos, cos, torch.ones(5, device=cuda), 2)
+    dq = torch.zeros(2, 2, 9, 16, device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.rope_merge(dq, dq[:, :1], dq, cos, cos, none)
+    with pytest.raises(ValueError):
+        torch.ops.ebr_fused.rope_merge(dq, dq, dq, cos[:, :8], cos[:, :8], none)

@@ -116,3 +116,5 @@ def test_rope_split_argument_checks():
         rope_split(torch.zeros(2, 9, 3 * 18), torch.zeros(9, 18), torch.zeros(9, 18), 1)  # D % 4
     with pytest.raises(ValueError):
         rope_split(torch.zeros(2, 9, 48), torch.zeros(8, 16), torch.zeros(8, 16), 1)  # table rows != N
+    with pytest.raises(ValueError):
+        rope_split(torch.zeros(2, 9, 96), cos, cos, 2, torch.ones(3))  # qscale: one value per head
