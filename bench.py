@@ -236,8 +236,9 @@ def bb_kernel_name(cfg: dict) -> str:
     L, D, dt = cfg["L"], cfg["D"], cfg["dtype"]
     if L > 128:
         if dt != torch.float32 and D in (32, 64):
-            nw = 7 if cfg["B"] * cfg["H"] * -(-L // 112) >= 1024 else 4  # long_wide() in ebr_attn.hip
-            return f"k_bb_long_row<{DT_NAME[dt]}, {D}, {nw}, 64> + k_bb_long_col<{DT_NAME[dt]}, {D}, {nw}>"
+            wide = cfg["B"] * cfg["H"] * -(-L // 112) >= 1024  # long_wide() in ebr_attn.hip
+            nw, nwr = (7, 10) if wide else (4, 4)  # LONG_WAVES_WIDE, BB_ROW_WAVES_WIDE
+            return f"k_bb_long_row<{DT_NAME[dt]}, {D}, {nwr}, 64> + k_bb_long_col<{DT_NAME[dt]}, {D}, {nw}>"
         return f"k_bb_row<{DT_NAME[dt]}, {D}> + k_bb_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32

@@ -881,6 +881,10 @@ static bool long_wide(int64_t bh, int L) {
     return bh * ((L + rows - 1) / rows) >= 1024;
 }
 constexpr int BB_ROW_STAGE = 64;  // k_bb_long_row's stage depth (32 rows with three workgroups per CU was slower)
+// k_bb_long_row needs about 150 VGPRs, so a SIMD holds 3 of its waves and a CU one 8-wave workgroup: 10 compute waves
+// (+ the loader) fill the CU with one workgroup of 160 rows instead (Maze bwd_bwd 1.26 -> 1.18 ms, measured). The
+// other long kernels keep 7: their wider variants measured slower (bwd with 9: 0.51 -> 0.70 ms; fwd with 6 or 13).
+constexpr int BB_ROW_WAVES_WIDE = 10;
 static bool long_shape(const Args& a, int dp, bool grads) {
     if (a.L <= STAT_MAX || a.D != dp) return false;
     const int es = 2;
@@ -1054,12 +1058,19 @@ template <typename T, int DP> struct BbLaunch {
             if (long_shape(a, DP, true)) {  // streamed stages with a loader wave (k_bb_long_row, k_bb_long_col)
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
+                    constexpr int NWR = NW == LONG_WAVES_WIDE ? BB_ROW_WAVES_WIDE : NW;
+                    {  // the row kernel has a row blocking of its own; the col kernel reads only its statistics
+                        Args ar = a;
+                        using CR = LongCfg<T, DP, NWR>;
+                        plan_long(ar, bh, CR::ROWS);
+                        hipLaunchKernelGGL((k_bb_long_row<T, DP, NWR, BB_ROW_STAGE>), dim3((int)(bh * ar.nblk)),
+                                           dim3(CR::THREADS), 0, s, ar);
+                    }
+                    const int rc = launch_rc();
+                    if (rc) return rc;
                     using C = LongCfg<T, DP, NW>;
                     plan_long(a, bh, C::ROWS);
                     const dim3 grid((int)(bh * a.nblk)), block(C::THREADS);
-                    hipLaunchKernelGGL((k_bb_long_row<T, DP, NW, BB_ROW_STAGE>), grid, block, 0, s, a);
-                    const int rc = launch_rc();
-                    if (rc) return rc;
                     hipLaunchKernelGGL((k_bb_long_col<T, DP, NW>), grid, block, 0, s, a);
                     return launch_rc();
                 };

@@ -166,6 +166,13 @@ def test_config2_maze_bf16_full_size(cuda):
     _sampled(64, 8, 900, 64, torch.bfloat16, cuda, 12)
 
 
+@pytest.mark.parametrize("B,H,L,D,dtype", [(64, 8, 333, 32, torch.bfloat16), (48, 8, 517, 64, torch.float16)])
+def test_long_wide_grids_ragged_L(cuda, B, H, L, D, dtype):
+    """Grids large enough for the wide long-sequence workgroups (7 compute waves; 10 in the bwd_bwd row kernel, with
+    its own 160-row blocking), L not a multiple of any block or stage; 8 random slices checked."""
+    _sampled(B, H, L, D, dtype, cuda, 8, seed=L)
+
+
 def test_config4_shape_bf16(cuda):
     """Config 4's attention shape (L=100) on a reduced batch; all slices checked."""
     _case(40, 8, 100, 64, torch.bfloat16, cuda, seed=4)
