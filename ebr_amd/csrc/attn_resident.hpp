@@ -811,7 +811,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
 //   compute waves                           loader waves
 //   row pass (s)                            load every input row of n into registers
 //   --- barrier A: tiles complete, K, gK, V, gV (s) no longer read
-//   store hQ, hdO (s); col pass (s)         write K, gK, V, gV (n)
+//   store hQ, hdO (s); col pass (s)         write K, gK, V, gV (n); rowsum(dO o O) (n) into registers
 //   --- barrier B: tiles and Q, gQ, dO (s) no longer read
 //   store hK, hV (s)                        write Q, gQ, dO (n), rowsum(dO o O) (n), lse (n)
 //   --- barrier C: every region holds n
@@ -881,6 +881,7 @@ template <typename T, int DP, int NCH> struct BbLoader {
     StageLanes<DP, R::NPER> sl;
     RS k, gk, v, gv, q, gq, dO, o;
     float lse;
+    float dr[R::NPER];  // rowsum(dO o O) of the rows this lane's chunks belong to (prep_rest)
     int lw, lane;
     __device__ __forceinline__ BbLoader(int lw_, int lane_) : sl(lw_, R::NWL, lane_), lw(lw_), lane(lane_) {}
     __device__ __forceinline__ void fetch(const Args& a, int s) {
@@ -903,18 +904,27 @@ template <typename T, int DP, int NCH> struct BbLoader {
         v.put(smem + 2 * R::RB, L, sl, lw, R::NWL, lane);
         gv.put(smem + 3 * R::RB, L, sl, lw, R::NWL, lane);
     }
-    __device__ __forceinline__ void put_rest(unsigned char* smem, float* dr, float* lse2, int L) const {
+    // rowsum(dO o O) of the fetched rows, in registers: the row's NCK lanes hold its chunks of both. Runs while the
+    // compute waves are still in the col pass, so that put_rest after its barrier only writes LDS.
+    __device__ __forceinline__ void prep_rest() {
+        constexpr int NCK = Sw<DP>::NCK;
+#pragma unroll
+        for (int i = 0; i < R::NPER; ++i) {
+            float d = dot8<T>(dO.v[i], o.v[i]);
+#pragma unroll
+            for (int m = 1; m < NCK; m <<= 1) d += __shfl_xor(d, m);
+            dr[i] = d;
+        }
+    }
+    __device__ __forceinline__ void put_rest(unsigned char* smem, float* drl, float* lse2, int L) const {
         q.put(smem + 4 * R::RB, L, sl, lw, R::NWL, lane);
         gq.put(smem + 5 * R::RB, L, sl, lw, R::NWL, lane);
         dO.put(smem + 6 * R::RB, L, sl, lw, R::NWL, lane);
         constexpr int NCK = Sw<DP>::NCK;
 #pragma unroll
-        for (int i = 0; i < R::NPER; ++i) {  // rowsum(dO o O): the row's NCK lanes hold its chunks of both
-            float d = dot8<T>(dO.v[i], o.v[i]);
-#pragma unroll
-            for (int m = 1; m < NCK; m <<= 1) d += __shfl_xor(d, m);
+        for (int i = 0; i < R::NPER; ++i) {
             const int x = sl.x[i];
-            if (lane % NCK == 0) dr[x] = x < L ? d : 0.f;
+            if (lane % NCK == 0) drl[x] = x < L ? dr[i] : 0.f;
         }
         const int t = lw * 64 + lane;
         if (t < R::LP) lse2[t] = t < L ? lse * LOG2E : INFINITY;  // padded query rows: P = 0
@@ -947,6 +957,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         BbLoader<T, DP, NCH> ld(w.wave - R::NWC, w.lane);
         ld.fetch(a, s);
         ld.put_k4(smem, L);
+        ld.prep_rest();
         ld.put_rest(smem, drl, lsel, L);
         lds_barrier();
         while (true) {
@@ -954,7 +965,10 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             const bool more = n < nbh;  // uniform over the workgroup
             if (more) ld.fetch(a, n);
             lds_barrier();  // A
-            if (more) ld.put_k4(smem, L);
+            if (more) {
+                ld.put_k4(smem, L);
+                ld.prep_rest();
+            }
             lds_barrier();  // B
             if (!more) break;
             ld.put_rest(smem, drl, lsel, L);
@@ -971,6 +985,12 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     const int own = row0 + w.l16;
     const bool active = row0 < L;
     const LaneOff<T, DP> lo(w.l16, w.g);
+    // hK, hV of the previous slice, rounded and packed, stored once this slice's row pass is done: right after the
+    // col pass every workgroup on the chip stores at once while the loaders' fetch of the next slice is in flight,
+    // and the store issue stalls the compute waves.
+    u32x2 pend_k[LY::NT], pend_v[LY::NT];
+    int64_t pend_r = 0;
+    bool pend = false;
     lds_barrier();  // the first slice is in LDS
     while (true) {
         const int n = s + (int)gridDim.x;
@@ -1055,6 +1075,16 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         } else {
             zero_tile_rows<NCH>(T2, T1, Ta, R::TP, own, w.g);
         }
+        if (pend) {
+            T* pk = reinterpret_cast<T*>(a.out1) + pend_r;
+            T* pv = reinterpret_cast<T*>(a.out2) + pend_r;
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) {
+                *reinterpret_cast<u32x2*>(pk + 16 * t + 4 * w.g) = pend_k[t];
+                *reinterpret_cast<u32x2*>(pv + 16 * t + 4 * w.g) = pend_v[t];
+            }
+            pend = false;
+        }
         lds_barrier();  // A
         if (own < L) {
             const int64_t r = ((int64_t)s * L + own) * DP;
@@ -1084,8 +1114,18 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         lds_barrier();  // B
         if (own < L) {
             const int64_t r = ((int64_t)s * L + own) * DP;
-            store_rows<T, DP>(a.out1, r, hk, sc, DP, w.g);
-            store_rows<T, DP>(a.out2, r, hv, 1.f, DP, w.g);
+            if (more) {
+#pragma unroll
+                for (int t = 0; t < LY::NT; ++t) {
+                    pend_k[t] = pack4<T>(hk[t] * sc);
+                    pend_v[t] = pack4<T>(hv[t]);
+                }
+                pend_r = r;
+                pend = true;
+            } else {
+                store_rows<T, DP>(a.out1, r, hk, sc, DP, w.g);
+                store_rows<T, DP>(a.out2, r, hv, 1.f, DP, w.g);
+            }
         }
         if (!more) break;
         lds_barrier();  // C

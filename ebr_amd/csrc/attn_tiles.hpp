@@ -392,6 +392,17 @@ template <typename T> __device__ __forceinline__ void store4(T* p, f32x4 v) {
     }
 }
 
+// Four values rounded to a 16-bit type, packed as store4 writes them.
+template <typename T> __device__ __forceinline__ u32x2 pack4(f32x4 v) {
+    using V4 = typename ET<T>::v4;
+    V4 r;
+    r[0] = (T)v[0];
+    r[1] = (T)v[1];
+    r[2] = (T)v[2];
+    r[3] = (T)v[3];
+    return __builtin_bit_cast(u32x2, r);
+}
+
 template <typename T> __device__ __forceinline__ f32x4 load4(const T* p) {
     if constexpr (ET<T>::F32) {
         return *reinterpret_cast<const f32x4*>(p);
