@@ -53,6 +53,58 @@ template <typename T, int DP> struct LaneOff {
     }
 };
 
+// Row stores through LDS. A seq-contraction accumulator holds, in lane (row l16, group g), columns 16 t + 4 g .. + 3 of
+// the wave's 16 rows: stored directly, each instruction writes 32 bytes into each of 16 rows, and partial-row writes
+// move about half the bytes per second of whole-row writes (measured: 3.5 against 6.5 TB/s for a pure write). So the
+// wave writes its rounded rows into a private 16-row LDS area (16-byte chunks XOR-swizzled as in the regions) and reads
+// them back as whole rows, 16 bytes per lane, for the global stores.
+template <typename T, int DP> struct RowStage16 {
+    static constexpr int BYTES = 16 * Sw<DP>::ROWB;  // one wave's area
+};
+
+// Lanes exchange data through the area, which the next tensor reuses right after: wave barriers keep every write
+// before the reads and every read before the next writes (without them the compiler may let lanes that store nothing
+// skip their read and write the next tensor's values before the other lanes have read these; it did for D = 32).
+
+// ``pk[t]`` = columns 16 t + 4 g .. + 3 of row l16, rounded and packed (pack4). Rows row0 .. row0 + 15 of ``out``
+// (contiguous, DP elements per row) are written where row0 + r < L.
+template <typename T, int DP>
+__device__ __forceinline__ void store_rows_staged(void* out, int64_t row0_off, int nvalid, const u32x2 (&pk)[DP / 16],
+                                                  unsigned char* stage, int lane) {
+    using S = Sw<DP>;
+    const int l16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < DP / 16; ++t) {
+        const int c = 2 * t + (g >> 1);  // 16-byte chunk of columns 16 t + 4 g
+        *reinterpret_cast<u32x2*>(stage + l16 * S::ROWB + 16 * (c ^ S::swz(l16)) + 8 * (g & 1)) = pk[t];
+    }
+    __builtin_amdgcn_wave_barrier();
+    constexpr int NI = 16 / S::RPI;
+    u32x4 v[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int r = i * S::RPI + lane / S::NCK, c = lane % S::NCK;
+        v[i] = *reinterpret_cast<const u32x4*>(stage + r * S::ROWB + 16 * (c ^ S::swz(r)));
+    }
+    __builtin_amdgcn_wave_barrier();
+    T* o = reinterpret_cast<T*>(out) + row0_off;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int r = i * S::RPI + lane / S::NCK, c = lane % S::NCK;
+        if (r < nvalid) *reinterpret_cast<u32x4*>(o + r * DP + 8 * c) = v[i];
+    }
+}
+
+// The same from fp32 accumulators, each scaled by ``mul`` before rounding.
+template <typename T, int DP>
+__device__ __forceinline__ void store_acc_staged(void* out, int64_t row0_off, int nvalid, const f32x4 (&acc)[DP / 16],
+                                                 float mul, unsigned char* stage, int lane) {
+    u32x2 pk[DP / 16];
+#pragma unroll
+    for (int t = 0; t < DP / 16; ++t) pk[t] = pack4<T>(acc[t] * mul);
+    store_rows_staged<T, DP>(out, row0_off, nvalid, pk, stage, lane);
+}
+
 // Issue the loads of rows [0, Lp) of one (b, h) slice into ``region`` (Lp * ROWB bytes); waves split the 1 KB blocks.
 template <typename T, int DP>
 __device__ __forceinline__ void async_rows(unsigned char* region, const T* slice, int64_t srow, int L, int Lp, int wave,
@@ -141,7 +193,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     using LY = Lay<T, DP>;
     constexpr int Lp = NCH * CH;
     constexpr int RB = Lp * Sw<DP>::ROWB;
-    __shared__ __align__(1024) unsigned char smem[2 * RB];
+    // K, V | a row-store area per wave
+    __shared__ __align__(1024) unsigned char smem[2 * RB + 2 * NCH * RowStage16<T, DP>::BYTES];
     const WaveIds w = wave_ids();
     const int nw = w.nthr >> 6;
     const int bh = blockIdx.x;
@@ -199,11 +252,9 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Vr, C * CH, t, lo), pb);
     });
     lsum = xsum4(lsum);
-    if (own < L) {
-        const int64_t r = (int64_t)bh * L + own;
-        store_rows<T, DP>(a.out0, r * DP, acc, 1.f / lsum, DP, w.g);
-        if (w.g == 0) a.lse_out[r] = m * (1.f / LOG2E) + logf(lsum);
-    }
+    store_acc_staged<T, DP>(a.out0, ((int64_t)bh * L + row0) * DP, L - row0, acc, 1.f / lsum,
+                            smem + 2 * RB + w.wave * RowStage16<T, DP>::BYTES, w.lane);
+    if (own < L && w.g == 0) a.lse_out[(int64_t)bh * L + own] = m * (1.f / LOG2E) + logf(lsum);
 }
 
 // =====================================================================================================================
@@ -378,8 +429,9 @@ template <typename T, int DP, int NCH> struct BwdPipe {
     static constexpr int TB = LP * TP;            // one tile
     static constexpr int NWC = 2 * NCH;           // compute waves
     static constexpr int BUF = 4 * RB;            // K, V, Q, dO
-    // two buffers | P, dS tiles | lse * log2 e (two) | rowsum(dO o O) (two)
-    static constexpr int SMEM = 2 * BUF + 2 * TB + 4 * LP * 4;
+    static constexpr int STG = 2 * BUF + 2 * TB + 4 * LP * 4;  // byte offset of the compute waves' store areas
+    // two buffers | P, dS tiles | lse * log2 e (two) | rowsum(dO o O) (two) | a row-store area per compute wave
+    static constexpr int SMEM = STG + NWC * RowStage16<T, DP>::BYTES;
     static constexpr int THREADS = 64 * (NWC + 1);
     static constexpr bool FITS = SMEM <= 160 * 1024;
 };
@@ -502,6 +554,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     const int own = row0 + w.l16;
     const bool active = row0 < L;
     const LaneOff<T, DP> lo(w.l16, w.g);
+    unsigned char* stage = smem + R::STG + w.wave * RowStage16<T, DP>::BYTES;
     lds_barrier();  // the first slice is in buffer 0
     for (int it = 0;; ++it) {
         const int n = s + (int)gridDim.x;
@@ -551,7 +604,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
 #pragma unroll
                 for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, x0, t, lo), dsb);
             });
-            if (own < L) store_rows<T, DP>(a.out0, ((int64_t)s * L + own) * DP, acc, sc, DP, w.g);
+            store_acc_staged<T, DP>(a.out0, ((int64_t)s * L + row0) * DP, L - row0, acc, sc, stage, w.lane);
         } else {
             zero_tile_rows<NCH>(TPr, TSr, nullptr, R::TP, own, w.g);
         }
@@ -573,11 +626,9 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                     ak[t] = mma_seq<T>(ak[t], seqa_tr<T, DP>(Qr, x0, t, lo), dsb);
                 }
             });
-            if (own < L) {
-                const int64_t r = ((int64_t)s * L + own) * DP;
-                store_rows<T, DP>(a.out1, r, ak, sc, DP, w.g);
-                store_rows<T, DP>(a.out2, r, av, 1.f, DP, w.g);
-            }
+            const int64_t r = ((int64_t)s * L + row0) * DP;
+            store_acc_staged<T, DP>(a.out1, r, L - row0, ak, sc, stage, w.lane);
+            store_acc_staged<T, DP>(a.out2, r, L - row0, av, 1.f, stage, w.lane);
         }
         if (!more) break;
         lds_barrier();  // Y: this buffer and the tiles free, the other buffer holds slice n
@@ -828,8 +879,9 @@ template <typename T, int DP, int NCH> struct BbShare {
     static constexpr int NPER = NB / NWL;         // blocks per loader wave and tensor
     static_assert(NPER * NWL == NB, "the loader waves split every tensor's 1 KB blocks evenly");
     static_assert(NWL * 64 >= LP, "one loader lane per row for lse");
-    // K, gK, V, gV | Q, gQ, dO | dS2, dS, Pa | rowsum(dO o O), lse * log2 e
-    static constexpr int SMEM = 7 * RB + 3 * TB + 2 * LP * 4;
+    static constexpr int STG = 3 * TB + 7 * RB + 2 * LP * 4;  // byte offset of the compute waves' store areas
+    // K, gK, V, gV | Q, gQ, dO | dS2, dS, Pa | rowsum(dO o O), lse * log2 e | a row-store area per compute wave
+    static constexpr int SMEM = STG + NWC * RowStage16<T, DP>::BYTES;
     static constexpr int THREADS = 64 * (NWC + NWL);
 };
 
@@ -985,6 +1037,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     const int own = row0 + w.l16;
     const bool active = row0 < L;
     const LaneOff<T, DP> lo(w.l16, w.g);
+    unsigned char* stage = smem + R::STG + w.wave * RowStage16<T, DP>::BYTES;
     // hK, hV of the previous slice, rounded and packed, stored once this slice's row pass is done: right after the
     // col pass every workgroup on the chip stores at once while the loaders' fetch of the next slice is in flight,
     // and the store issue stalls the compute waves.
@@ -1075,21 +1128,16 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         } else {
             zero_tile_rows<NCH>(T2, T1, Ta, R::TP, own, w.g);
         }
-        if (pend) {
-            T* pk = reinterpret_cast<T*>(a.out1) + pend_r;
-            T* pv = reinterpret_cast<T*>(a.out2) + pend_r;
-#pragma unroll
-            for (int t = 0; t < LY::NT; ++t) {
-                *reinterpret_cast<u32x2*>(pk + 16 * t + 4 * w.g) = pend_k[t];
-                *reinterpret_cast<u32x2*>(pv + 16 * t + 4 * w.g) = pend_v[t];
-            }
+        if (pend) {  // wave-uniform
+            store_rows_staged<T, DP>(a.out1, pend_r, L - row0, pend_k, stage, w.lane);
+            store_rows_staged<T, DP>(a.out2, pend_r, L - row0, pend_v, stage, w.lane);
             pend = false;
         }
         lds_barrier();  // A
-        if (own < L) {
-            const int64_t r = ((int64_t)s * L + own) * DP;
-            store_rows<T, DP>(a.out0, r, hq, sc, DP, w.g);
-            store_rows<T, DP>(a.out3, r, hdo, 1.f, DP, w.g);
+        if (active) {
+            const int64_t r = ((int64_t)s * L + row0) * DP;
+            store_acc_staged<T, DP>(a.out0, r, L - row0, hq, sc, stage, w.lane);
+            store_acc_staged<T, DP>(a.out3, r, L - row0, hdo, 1.f, stage, w.lane);
         }
 
         // ---- col pass: own = keys; hK, hV from the tiles
@@ -1112,8 +1160,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             });
         }
         lds_barrier();  // B
-        if (own < L) {
-            const int64_t r = ((int64_t)s * L + own) * DP;
+        if (active) {
+            const int64_t r = ((int64_t)s * L + row0) * DP;
             if (more) {
 #pragma unroll
                 for (int t = 0; t < LY::NT; ++t) {
@@ -1123,8 +1171,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 pend_r = r;
                 pend = true;
             } else {
-                store_rows<T, DP>(a.out1, r, hk, sc, DP, w.g);
-                store_rows<T, DP>(a.out2, r, hv, 1.f, DP, w.g);
+                store_acc_staged<T, DP>(a.out1, r, L - row0, hk, sc, stage, w.lane);
+                store_acc_staged<T, DP>(a.out2, r, L - row0, hv, 1.f, stage, w.lane);
             }
         }
         if (!more) break;
