@@ -193,8 +193,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     using LY = Lay<T, DP>;
     constexpr int Lp = NCH * CH;
     constexpr int RB = Lp * Sw<DP>::ROWB;
-    // K, V | a row-store area per wave
-    __shared__ __align__(1024) unsigned char smem[2 * RB + 2 * NCH * RowStage16<T, DP>::BYTES];
+    // K, V | a row-store area per wave, unless it would leave room for fewer than two workgroups per CU (D = 128,
+    // L > 96: the stores then go out directly)
+    constexpr int STG = 2 * NCH * RowStage16<T, DP>::BYTES;
+    constexpr bool STAGED = 2 * (2 * RB + STG) <= 160 * 1024;
+    __shared__ __align__(1024) unsigned char smem[2 * RB + (STAGED ? STG : 0)];
     const WaveIds w = wave_ids();
     const int nw = w.nthr >> 6;
     const int bh = blockIdx.x;
@@ -252,8 +255,12 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Vr, C * CH, t, lo), pb);
     });
     lsum = xsum4(lsum);
-    store_acc_staged<T, DP>(a.out0, ((int64_t)bh * L + row0) * DP, L - row0, acc, 1.f / lsum,
-                            smem + 2 * RB + w.wave * RowStage16<T, DP>::BYTES, w.lane);
+    if constexpr (STAGED) {
+        store_acc_staged<T, DP>(a.out0, ((int64_t)bh * L + row0) * DP, L - row0, acc, 1.f / lsum,
+                                smem + 2 * RB + w.wave * RowStage16<T, DP>::BYTES, w.lane);
+    } else if (own < L) {
+        store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * DP, acc, 1.f / lsum, DP, w.g);
+    }
     if (own < L && w.g == 0) a.lse_out[(int64_t)bh * L + own] = m * (1.f / LOG2E) + logf(lsum);
 }
 
