@@ -104,9 +104,11 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
                 for (int r = 0; r < 4; ++r)
                     if (kb + 16 * kt + 4 * w.g + r >= L) s[kt][r] = -INFINITY;
         }
-        float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+        float mx = s[0][0];
 #pragma unroll
-        for (int kt = 1; kt < 4; ++kt) mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = (kt == 0 ? 1 : 0); r < 4; ++r) mx = fmax_nn(mx, s[kt][r]);
         // Every stage holds at least one key below L, so the stage maximum is finite. The reference point m moves
         // only when some row's maximum exceeds it by more than RESCALE_SLACK (wave vote): P stays <= 2^SLACK, and
         // the accumulator is rescaled a few times per row instead of at every stage.
@@ -214,43 +216,53 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         const unsigned char* Kr = smem + (i & 1) * STB;
         const unsigned char* Vr = Kr + C::SB;
         const int kb = i * LSTAGE;
-        const bool last = kb + LSTAGE > L;
+        // Keys past L (zero rows in the stage) are masked in the last stage only: a branch per stage, so that the
+        // other stages carry no compare / select work.
+        auto stage = [&](auto lastc) {
+            constexpr bool LAST = decltype(lastc)::value;
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            f32x4 p[2], dp[2];
+            for (int c = 0; c < 2; ++c) {
+                f32x4 p[2], dp[2];
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                p[hh] = dp[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
-                u32x4 ka[LY::NC], va[LY::NC];
+                for (int hh = 0; hh < 2; ++hh) {
+                    p[hh] = dp[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    u32x4 ka[LY::NC], va[LY::NC];
 #pragma unroll
-                for (int q = 0; q < LY::NC; ++q) {
-                    const int o = (32 * c + 16 * hh) * Sw<DP>::ROWB + lo.a[q];
-                    ka[q] = *reinterpret_cast<const u32x4*>(Kr + o);
-                    va[q] = *reinterpret_cast<const u32x4*>(Vr + o);
+                    for (int q = 0; q < LY::NC; ++q) {
+                        const int o = (32 * c + 16 * hh) * Sw<DP>::ROWB + lo.a[q];
+                        ka[q] = *reinterpret_cast<const u32x4*>(Kr + o);
+                        va[q] = *reinterpret_cast<const u32x4*>(Vr + o);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int q = 0; q < LY::NC; ++q) {
+                        p[hh] = ET<T>::mma(ka[q], qf.v[q], p[hh]);
+                        dp[hh] = ET<T>::mma(va[q], df.v[q], dp[hh]);
+                    }
                 }
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
+                        if constexpr (LAST) {
+                            if (kb + 32 * c + 16 * hh + 4 * w.g + r >= L) pv = 0.f;
+                        }
+                        p[hh][r] = pv * (dp[hh][r] - dr);  // dS
+                    }
+                const SeqB<T> dsb = make_seqb<T>(p[0], p[1]);
+                SeqA<T> kt[LY::NT];
+#pragma unroll
+                for (int t = 0; t < LY::NT; ++t) kt[t] = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int q = 0; q < LY::NC; ++q) {
-                    p[hh] = ET<T>::mma(ka[q], qf.v[q], p[hh]);
-                    dp[hh] = ET<T>::mma(va[q], df.v[q], dp[hh]);
-                }
+                for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], kt[t], dsb);
             }
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
-                    if (last && kb + 32 * c + 16 * hh + 4 * w.g + r >= L) pv = 0.f;
-                    p[hh][r] = pv * (dp[hh][r] - dr);  // dS
-                }
-            const SeqB<T> dsb = make_seqb<T>(p[0], p[1]);
-            SeqA<T> kt[LY::NT];
-#pragma unroll
-            for (int t = 0; t < LY::NT; ++t) kt[t] = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], kt[t], dsb);
-        }
+        };
+        if (kb + LSTAGE > L)
+            stage(std::true_type{});
+        else
+            stage(std::false_type{});
     }
     if (active && own < L) store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * DP, acc, a.scale, DP, w.g);
 }
@@ -424,82 +436,91 @@ __global__ __launch_bounds__(64 * (NWC + 1)) void k_bb_long_row(Args a) {
         const unsigned char* Vr = Kr + 2 * SB;
         const unsigned char* gVr = Kr + 3 * SB;
         const int kb = i * STG;
-        const bool last = kb + STG > L;
+        // Keys past L are masked in the last stage only (a branch per stage, no compare / select work elsewhere).
+        auto stage = [&](auto lastc) {
+            constexpr bool LAST = decltype(lastc)::value;
 #pragma unroll
-        for (int c = 0; c < STG / CH; ++c) {
-            f32x4 p[2], at[2], dp[2], bm[2];
+            for (int c = 0; c < STG / CH; ++c) {
+                f32x4 p[2], at[2], dp[2], bm[2];
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                p[hh] = at[hh] = dp[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
-                const int r0 = 32 * c + 16 * hh;
-                {
-                    u32x4 ka[LY::NC], gka[LY::NC];
+                for (int hh = 0; hh < 2; ++hh) {
+                    p[hh] = at[hh] = dp[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    const int r0 = 32 * c + 16 * hh;
+                    {
+                        u32x4 ka[LY::NC], gka[LY::NC];
 #pragma unroll
-                    for (int q = 0; q < LY::NC; ++q) {
-                        const int o = r0 * Sw<DP>::ROWB + lo.a[q];
-                        ka[q] = *reinterpret_cast<const u32x4*>(Kr + o);
-                        gka[q] = *reinterpret_cast<const u32x4*>(gKr + o);
+                        for (int q = 0; q < LY::NC; ++q) {
+                            const int o = r0 * Sw<DP>::ROWB + lo.a[q];
+                            ka[q] = *reinterpret_cast<const u32x4*>(Kr + o);
+                            gka[q] = *reinterpret_cast<const u32x4*>(gKr + o);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int q = 0; q < LY::NC; ++q) {
+                            p[hh] = ET<T>::mma(ka[q], qf.v[q], p[hh]);
+                            at[hh] = ET<T>::mma(ka[q], gqf.v[q], at[hh]);
+                            at[hh] = ET<T>::mma(gka[q], qf.v[q], at[hh]);
+                        }
                     }
-                    __builtin_amdgcn_sched_barrier(0);
+                    {
+                        u32x4 va[LY::NC], gva[LY::NC];
 #pragma unroll
-                    for (int q = 0; q < LY::NC; ++q) {
-                        p[hh] = ET<T>::mma(ka[q], qf.v[q], p[hh]);
-                        at[hh] = ET<T>::mma(ka[q], gqf.v[q], at[hh]);
-                        at[hh] = ET<T>::mma(gka[q], qf.v[q], at[hh]);
+                        for (int q = 0; q < LY::NC; ++q) {
+                            const int o = r0 * Sw<DP>::ROWB + lo.a[q];
+                            va[q] = *reinterpret_cast<const u32x4*>(Vr + o);
+                            gva[q] = *reinterpret_cast<const u32x4*>(gVr + o);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int q = 0; q < LY::NC; ++q) {
+                            dp[hh] = ET<T>::mma(va[q], df.v[q], dp[hh]);
+                            bm[hh] = ET<T>::mma(gva[q], df.v[q], bm[hh]);
+                        }
                     }
                 }
-                {
-                    u32x4 va[LY::NC], gva[LY::NC];
 #pragma unroll
-                    for (int q = 0; q < LY::NC; ++q) {
-                        const int o = r0 * Sw<DP>::ROWB + lo.a[q];
-                        va[q] = *reinterpret_cast<const u32x4*>(Vr + o);
-                        gva[q] = *reinterpret_cast<const u32x4*>(gVr + o);
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
+                        if constexpr (LAST) {
+                            if (kb + 32 * c + 16 * hh + 4 * w.g + r >= L) pv = 0.f;
+                        }
+                        const float dsv = pv * (dp[hh][r] - dr);
+                        const float av = at[hh][r] * sc;
+                        const float pa = pv * av;
+                        const float m1 = fmaf(dsv, av, pv * bm[hh][r]);
+                        e_acc += pa;
+                        t_acc += m1;
+                        p[hh][r] = pv;
+                        dp[hh][r] = dsv;
+                        at[hh][r] = pa;
+                        bm[hh][r] = m1;
                     }
+                const SeqB<T> pb = make_seqb<T>(p[0], p[1]);
+                const SeqB<T> dsb = make_seqb<T>(dp[0], dp[1]);
+                const SeqB<T> pab = make_seqb<T>(at[0], at[1]);
+                const SeqB<T> m1b = make_seqb<T>(bm[0], bm[1]);
+#pragma unroll
+                for (int t = 0; t < LY::NT; ++t) {
+                    const SeqA<T> kt = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
+                    const SeqA<T> gkt = seqa_tr<T, DP>(gKr, 32 * c, t, lo);
+                    const SeqA<T> vt = seqa_tr<T, DP>(Vr, 32 * c, t, lo);
+                    const SeqA<T> gvt = seqa_tr<T, DP>(gVr, 32 * c, t, lo);
                     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int q = 0; q < LY::NC; ++q) {
-                        dp[hh] = ET<T>::mma(va[q], df.v[q], dp[hh]);
-                        bm[hh] = ET<T>::mma(gva[q], df.v[q], bm[hh]);
-                    }
+                    X[t] = mma_seq<T>(X[t], kt, m1b);
+                    X[t] = mma_seq<T>(X[t], gkt, dsb);
+                    U[t] = mma_seq<T>(U[t], kt, dsb);
+                    Z[t] = mma_seq<T>(Z[t], kt, pb);
+                    W[t] = mma_seq<T>(W[t], vt, pab);
+                    W[t] = mma_seq<T>(W[t], gvt, pb);
                 }
             }
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
-                    if (last && kb + 32 * c + 16 * hh + 4 * w.g + r >= L) pv = 0.f;
-                    const float dsv = pv * (dp[hh][r] - dr);
-                    const float av = at[hh][r] * sc;
-                    const float pa = pv * av;
-                    const float m1 = fmaf(dsv, av, pv * bm[hh][r]);
-                    e_acc += pa;
-                    t_acc += m1;
-                    p[hh][r] = pv;
-                    dp[hh][r] = dsv;
-                    at[hh][r] = pa;
-                    bm[hh][r] = m1;
-                }
-            const SeqB<T> pb = make_seqb<T>(p[0], p[1]);
-            const SeqB<T> dsb = make_seqb<T>(dp[0], dp[1]);
-            const SeqB<T> pab = make_seqb<T>(at[0], at[1]);
-            const SeqB<T> m1b = make_seqb<T>(bm[0], bm[1]);
-#pragma unroll
-            for (int t = 0; t < LY::NT; ++t) {
-                const SeqA<T> kt = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
-                const SeqA<T> gkt = seqa_tr<T, DP>(gKr, 32 * c, t, lo);
-                const SeqA<T> vt = seqa_tr<T, DP>(Vr, 32 * c, t, lo);
-                const SeqA<T> gvt = seqa_tr<T, DP>(gVr, 32 * c, t, lo);
-                __builtin_amdgcn_sched_barrier(0);
-                X[t] = mma_seq<T>(X[t], kt, m1b);
-                X[t] = mma_seq<T>(X[t], gkt, dsb);
-                U[t] = mma_seq<T>(U[t], kt, dsb);
-                Z[t] = mma_seq<T>(Z[t], kt, pb);
-                W[t] = mma_seq<T>(W[t], vt, pab);
-                W[t] = mma_seq<T>(W[t], gvt, pb);
-            }
-        }
+        };
+        if (kb + STG > L)
+            stage(std::true_type{});
+        else
+            stage(std::false_type{});
     }
     if (!active) return;
     const float E = xsum4(e_acc);

@@ -231,7 +231,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 if constexpr (C == NCH - 1) {
                     if (C * CH + 16 * hh + 4 * w.g + r >= L) v[r] = -INFINITY;
                 }
-                mx = fmaxf(mx, v[r]);
+                mx = fmax_nn(mx, v[r]);
             }
             s[2 * C + hh] = v;
         }

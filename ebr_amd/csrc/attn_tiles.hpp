@@ -100,16 +100,38 @@ template <typename T> __device__ __forceinline__ int tr_col(int x) {
 // Lane reductions over the four 16-lane groups (lanes l, l^16, l^32, l^48 hold the same own row).
 // ---------------------------------------------------------------------------------------------------------------------
 
+// gfx950's v_permlane16_swap / v_permlane32_swap exchange 16-lane rows between two registers without LDS. Called
+// with the same register twice, every lane ends up holding its own value in one result and the value of lane
+// l ^ 16 (l ^ 32) in the other, so one swap and one VALU op reduce over a lane pair. The same pairs and order as a
+// shuffle-xor reduction: the sums are bit-identical to it.
+__device__ __forceinline__ void xpair16(float v, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ void xpair32(float v, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+// max(a, b) for values that are never NaN (scores, -inf for masked keys): med3(a, b, +inf) selects v_max3_f32
+// chains without the NaN-quieting copies that fmaxf adds to MFMA results.
+__device__ __forceinline__ float fmax_nn(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, INFINITY); }
+
 __device__ __forceinline__ float xsum4(float v) {
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+    float a, b;
+    xpair16(v, a, b);
+    xpair32(a + b, a, b);
+    return a + b;
 }
 
 __device__ __forceinline__ float xmax4(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
+    float a, b;
+    xpair16(v, a, b);
+    xpair32(fmax_nn(a, b), a, b);
+    return fmax_nn(a, b);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
