@@ -645,14 +645,14 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
                 const f32x4 t2 = *reinterpret_cast<const f32x4*>(st + 3 * LSTAGE + x);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
+                    // With E and T known, dS2 = dS (A - E) + P (Bm - T) and Pa = P (A - E): the centred forms of
+                    // dS o A + P o Bm - E dS - T P and P o A - E P, two VALU operations fewer per element.
                     const float pv = fast_exp2(fmaf(p[hh][r], sc2, -l2[r]));  // lse = +inf past L: P = 0
                     const float dsv = pv * (dp[hh][r] - d2[r]);
-                    const float av = at[hh][r] * sc;
-                    const float pa = pv * av;
-                    const float m1 = fmaf(dsv, av, pv * bm[hh][r]);
-                    p[hh][r] = m1 - e2[r] * dsv - t2[r] * pv;  // dS2
+                    const float ae = fmaf(at[hh][r], sc, -e2[r]);
+                    p[hh][r] = fmaf(dsv, ae, pv * (bm[hh][r] - t2[r]));  // dS2
                     dp[hh][r] = dsv;
-                    at[hh][r] = pa - e2[r] * pv;  // Pa
+                    at[hh][r] = pv * ae;  // Pa
                 }
             }
             const SeqB<T> d2b = make_seqb<T>(p[0], p[1]);
