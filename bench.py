@@ -371,7 +371,24 @@ def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
     torch.cuda.synchronize()
     gc.unfreeze()
     ms = e0.elapsed_time(e1) / steps
+    # The same step captured in a HIP graph over the same static inputs: each step is one graph launch, with no
+    # Python, autograd or launch work on the host (the eager step above waits on the host for part of its time).
+    model.zero_grad(set_to_none=True)
+    dec.zero_grad(set_to_none=True)
+    graph, gloss = en.graph_train_step(model, dec, x, z0, tg)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    gms = e0.elapsed_time(e1) / steps
+    graphed = {"steps_per_s": round(1000.0 / gms, 3), "ms_per_step": round(gms, 2), "loss": round(float(gloss), 4),
+               "loss_equals_eager": bool(torch.equal(gloss, loss))}
+    del graph
     out = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 2), "loss": round(float(loss), 4),
+           "graph": graphed,
            "config": "B=384 L=81 hidden=512 heads=8x64 layers=2 SwiGLU x4, 16 create_graph descent steps, bf16; 2D RoPE "
                      "by the fused split/merge (the reference's Sudoku recipe), rms_norm and SwiGLU activation by the "
                      "fused block kernels, projection weight gradients as split-K GEMMs with fp32 partials; Python's "

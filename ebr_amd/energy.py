@@ -285,6 +285,27 @@ def train_step(model, decoder, x, z0, targets, steps: int = 16, alpha=0.1, compi
     return loss.detach()
 
 
+def graph_train_step(model, decoder, x, z0, targets, steps: int = 16, alpha=0.1, warmup: int = 2):
+    """``train_step`` captured in a HIP graph over static inputs ``x``, ``z0``, ``targets`` (config 3 with the fused
+    kernels: every launch goes to torch's current stream, nothing synchronises with the host, no allocation outside
+    torch's allocator). Returns ``(graph, loss)``: ``graph.replay()`` re-runs the whole step (graded descent, CE,
+    backward) on the inputs' current contents and writes ``loss`` and every parameter's ``.grad`` in place (the
+    gradients are assigned, not accumulated: they are allocated by the captured backward). Warm-up steps run on a side
+    stream first, as capture needs (the attention self-test and the allocator's pools settle there)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(warmup):
+            train_step(model, decoder, x, z0, targets, steps, alpha)
+            model.zero_grad(set_to_none=True)
+            decoder.zero_grad(set_to_none=True)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        loss = train_step(model, decoder, x, z0, targets, steps, alpha)
+    return graph, loss
+
+
 @torch.no_grad()
 def _energies(model, v, x_emb):
     return model(v, x_emb)
@@ -323,6 +344,7 @@ __all__ = [
     "compiled_energy_grad",
     "descend",
     "energy_grad",
+    "graph_train_step",
     "infer",
     "microstep",
     "sphere",

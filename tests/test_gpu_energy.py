@@ -99,3 +99,35 @@ def test_compiled_energy_grad_matches_eager(cuda):
     ve = en.descend(model, z0, x_emb, 4, 0.1, create_graph=False)
     vc, ve = vc.detach(), ve.detach()
     assert float((vc - ve).abs().max()) <= 1e-4 * float(ve.abs().max())
+
+
+def test_graph_train_step_replays_match_eager(cuda):
+    """The config-3 step (fused RoPE, block and split-K gradients, bf16) captured in a HIP graph: three replays, each
+    on new latents copied into the static input and with eager steps of a twin model run between the replays, give
+    the eager step's loss and gradients on the same inputs."""
+    print("[case] graph-captured train step bf16", flush=True)
+    kw = dict(hidden_size=128, num_heads=2, grid=(9, 9), attn_backend="fused", attn_nograd_backend="fused",
+              rope_impl="fused", block_impl="fused", linear_impl="splitk")
+    mg, dg = en.build(en.EnergyConfig(**kw), cuda, seed=5)
+    me, de = en.build(en.EnergyConfig(**kw), cuda, seed=5)
+    g = torch.Generator("cpu").manual_seed(6)
+    B, L = 4, 81
+    x = torch.randint(0, 11, (B, L), generator=g).to(cuda)
+    tg = torch.randint(0, 11, (B, L), generator=g).to(cuda)
+    z0 = torch.randn(B, L, 128, generator=g).to(cuda, torch.bfloat16)
+    graph, loss = en.graph_train_step(mg, dg, x, z0, tg, steps=3)
+    for rep in range(3):
+        z0.copy_(torch.randn(B, L, 128, generator=g).to(cuda, torch.bfloat16))
+        graph.replay()
+        me.zero_grad(set_to_none=True)
+        de.zero_grad(set_to_none=True)
+        le = en.train_step(me, de, x, z0, tg, steps=3)  # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(loss) and abs(float(loss) - float(le)) <= 1e-4 * abs(float(le)), (rep, loss, le)
+        for (n, pg), (_, pe) in zip((*mg.named_parameters(), *dg.named_parameters()),
+                                    (*me.named_parameters(), *de.named_parameters())):
+            if pe.grad is None:
+                assert pg.grad is None, n
+                continue
+            err = float((pg.grad.float() - pe.grad.float()).abs().max() / pe.grad.float().abs().max().clamp_min(1e-12))
+            assert err <= 1e-3, (rep, n, err)
