@@ -10,6 +10,8 @@ import os
 import shutil
 import subprocess
 import sys
+import time
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -40,12 +42,12 @@ def hipcc() -> str:
 
 
 def compile_flags(arch: str = ARCH) -> list:
+    """Flags of every HIP translation unit (compiled to an object each, then linked into the shared library)."""
     return [
         f"--offload-arch={arch}",
         "-O3",
         "-std=c++17",
         "-fPIC",
-        "-shared",
         "-Wall",
         "-Wno-unused-function",
         "-Xclang",
@@ -56,20 +58,39 @@ def compile_flags(arch: str = ARCH) -> list:
     ]
 
 
-def build(verbose: bool = False, extra_flags: tuple = ()) -> Path:
-    """Compile every HIP source into the in-tree shared library and return its path."""
-    OUT_DIR.mkdir(parents=True, exist_ok=True)
-    out = OUT_DIR / LIB_NAME
-    tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc(), *compile_flags(), *extra_flags, *map(str, SOURCES), "-o", str(tmp)]
+def _run(cmd: list, verbose: bool) -> str:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
-    if verbose and proc.stderr.strip():
-        sys.stderr.write(proc.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}: {' '.join(cmd[-3:])}")
+    return proc.stderr
+
+
+def build(verbose: bool = False, extra_flags: tuple = (), jobs: int = 0) -> Path:
+    """Compile every HIP source (in parallel, one object each) and link the in-tree shared library; return its path."""
+    OUT_DIR.mkdir(parents=True, exist_ok=True)
+    out = OUT_DIR / LIB_NAME
+    tmp = out.with_suffix(".so.tmp")
+    obj_dir = OUT_DIR / "obj"
+    obj_dir.mkdir(exist_ok=True)
+    cc = hipcc()
+    flags = [*compile_flags(), *extra_flags]
+    objs = [obj_dir / (src.stem + ".o") for src in SOURCES]
+    t0 = time.time()
+    workers = jobs or min(len(SOURCES), max(1, os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        logs = list(pool.map(lambda so: _run([cc, *flags, "-c", str(so[0]), "-o", str(so[1])], verbose),
+                             zip(SOURCES, objs)))
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
+    if verbose:
+        noise = "is not a recognized feature for this target"
+        for log in logs:
+            lines = [ln for ln in log.splitlines() if noise not in ln]
+            if lines:
+                sys.stderr.write("\n".join(lines) + "\n")
+        print(f"built in {time.time() - t0:.1f} s", flush=True)
     os.replace(tmp, out)
     return out
 

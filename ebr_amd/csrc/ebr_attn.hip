@@ -24,8 +24,6 @@
 #include <stdint.h>
 
 #include <cmath>
-#include <map>
-#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -819,34 +817,19 @@ static int launch_rc() {
     return e == hipSuccess ? EBR_OK : EBR_ERR_HIP_BASE + (int)e;
 }
 
-// Grid of a persistent kernel: as many workgroups as the current device holds at once (at most ``work``), cached per
-// kernel and device. One workgroup per work item when the runtime cannot tell (the kernels are correct at any grid).
+// Grid of a persistent kernel: as many workgroups as the current device holds at once (at most ``work``). Queried on
+// every call (device attribute and the kernel's occupancy, host-side lookups that enqueue nothing), so the library
+// keeps no state between calls. One workgroup per work item when the runtime cannot tell: the kernels are correct at
+// any grid.
 static int persistent_grid(const void* kernel, int threads, int64_t work) {
-    static std::mutex mu;
-    static std::map<std::pair<const void*, int>, int> slots_of;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) {
+    int dev = 0, ncu = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || ncu < 1 || per < 1) {
         (void)hipGetLastError();
         return (int)work;
     }
-    int slots = 0;
-    {
-        std::lock_guard<std::mutex> lk(mu);
-        const auto it = slots_of.find({kernel, dev});
-        if (it != slots_of.end()) slots = it->second;
-    }
-    if (slots == 0) {
-        int ncu = 0, per = 0;
-        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || ncu < 1 ||
-            per < 1) {
-            (void)hipGetLastError();
-            return (int)work;
-        }
-        slots = ncu * per;
-        std::lock_guard<std::mutex> lk(mu);
-        slots_of[{kernel, dev}] = slots;
-    }
+    const int64_t slots = (int64_t)ncu * per;
     return (int)(work < slots ? work : slots);
 }
 

@@ -1,12 +1,13 @@
-"""Selection of the fused attention implementation (mirrors reference ``models/fused_attn/loader.py:1-36``).
+"""Selection of the fused attention implementation (the reference's ``models/fused_attn/loader.py:1-36`` contract).
 
 ``EBR_FUSED_ATTN_IMPL``:
-- ``auto`` (default), ``hip``: the gfx950 HIP library ``libebr_attn.so``. If it cannot be loaded the op raises
-  ``RuntimeError`` naming the reason. Unlike the reference's ``auto``, there is no dense fallback: this build ships
-  only the HIP kernels, so a missing library is an error, never a silent change of implementation.
-- ``triton``: accepted as an alias of ``hip`` (the reference's "kernel or error" mode, which training scripts export).
-- ``reference``: the reference forces its dense PyTorch path here; this build has none to force and raises
-  ``RuntimeError``. Use the ``math`` attention backend for an eager path.
+- ``auto`` (default) and ``hip``: GPU tensors run the gfx950 HIP library ``libebr_attn.so``; tensors off the GPU run
+  the dense torch functions. If the library cannot be loaded, a GPU call raises ``RuntimeError`` naming the reason.
+  The reference's ``auto`` would fall back to its dense functions on the GPU instead; here a GPU caller never gets
+  another implementation than the one it asked for without being told.
+- ``triton``: the reference's "kernels or an error" mode, which its training scripts export
+  (``scripts/train.sh:15``); here the same as ``hip``.
+- ``reference``: the dense torch functions for every tensor, on the GPU too (the reference's forced dense path).
 """
 
 from __future__ import annotations
@@ -26,20 +27,17 @@ def mode() -> str:
 
 
 def hip_library():
-    """The loaded ``libebr_attn.so`` (ctypes), or RuntimeError when the selected mode cannot provide it."""
-    m = mode()
-    if m == "reference":
-        raise RuntimeError(
-            "EBR_FUSED_ATTN_IMPL=reference: this build ships no dense fused-attention fallback; "
-            "select the 'math' attention backend for the eager path"
-        )
+    """The loaded ``libebr_attn.so`` (ctypes), or RuntimeError naming why it cannot be loaded."""
     try:
         return _capi.load()
     except RuntimeError as exc:
-        raise RuntimeError(f"EBR_FUSED_ATTN_IMPL={m}: the gfx950 fused attention library is unavailable: {exc}") from exc
+        raise RuntimeError(
+            f"EBR_FUSED_ATTN_IMPL={mode()}: the gfx950 fused attention library is unavailable: {exc}"
+        ) from exc
 
 
 def available() -> bool:
+    """Whether the HIP library loads (it does not say whether a GPU is present)."""
     try:
         hip_library()
         return True

@@ -2,9 +2,10 @@
 implementation selector and the second-order self-test (reference models/fused_attn/ops.py, loader.py and
 models/attention.py:89-173).
 
-The shipped ops have a HIP kernel only. These tests register a test-local CPU kernel for them that wraps the CPU
-oracle (with a switch that plants a mistake), so the wiring can be exercised without a GPU. The CPU kernel never ships:
-it exists only inside this test module.
+On CPU tensors the ops run the package's dense path (``ebr_amd/fused_attn/dense.py``), as the reference's ops run its
+dense functions there (ops.py:68-70); every value is compared with the CPU oracle or with torch autograd. Calls are
+counted by wrapping the dense functions; the one planted mistake lives in a test-only attention backend built from
+the oracle.
 """
 
 import os
@@ -15,50 +16,27 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 
 import oracle
 from ebr_amd import attention as att
-from ebr_amd.fused_attn import loader, ops
+from ebr_amd.fused_attn import dense, loader, ops
 
 F64 = torch.float64
-PLANT = {"bwd_bwd_scale": 1.0, "detach": False, "calls": []}
 
 
-def _cpu_fwd(q, k, v, scale):
-    PLANT["calls"].append("fwd")
-    o, lse = oracle.attn_fwd(q, k, v, scale)
-    return o.contiguous(), lse.to(ops.lse_dtype_for(q)).contiguous()
+@pytest.fixture
+def calls(monkeypatch):
+    """Records every dense call the ops make (name and, for bwd_bwd, the cotangents' strides)."""
+    seen = []
 
+    def wrap(name, fn, strides=False):
+        def run(*args):
+            seen.append((name, tuple(a.stride() for a in args[6:9])) if strides else name)
+            return fn(*args)
 
-def _cpu_bwd(q, k, v, o, lse, do, scale):
-    PLANT["calls"].append("bwd")
-    dq, dk, dv = oracle.attn_bwd(q, k, v, o, lse, do, scale)
-    return dq.contiguous(), dk.contiguous(), dv.contiguous()
+        return run
 
-
-def _cpu_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale):
-    PLANT["calls"].append(("bwd_bwd", gq.stride(), gk.stride(), gv.stride()))
-    hq, hk, hv, hdo = oracle.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
-    f = PLANT["bwd_bwd_scale"]
-    return (hq * f).contiguous(), hk.contiguous(), hv.contiguous(), hdo.contiguous()
-
-
-_REGISTERED = False
-
-
-@pytest.fixture(scope="module", autouse=True)
-def cpu_kernels():
-    global _REGISTERED
-    if not _REGISTERED:
-        ops.attn_fwd.register_kernel("cpu")(_cpu_fwd)
-        ops.attn_bwd.register_kernel("cpu")(_cpu_bwd)
-        ops.attn_bwd_bwd.register_kernel("cpu")(_cpu_bwd_bwd)
-        _REGISTERED = True
-    yield
-
-
-@pytest.fixture(autouse=True)
-def reset_plant():
-    PLANT.update(bwd_bwd_scale=1.0, detach=False, calls=[])
-    yield
-    PLANT.update(bwd_bwd_scale=1.0, detach=False, calls=[])
+    monkeypatch.setattr(dense, "attn_fwd", wrap("fwd", dense.attn_fwd))
+    monkeypatch.setattr(dense, "attn_bwd", wrap("bwd", dense.attn_bwd))
+    monkeypatch.setattr(dense, "attn_bwd_bwd", wrap("bwd_bwd", dense.attn_bwd_bwd, strides=True))
+    return seen
 
 
 def _inputs(B=2, H=2, L=9, D=8, dtype=F64, seed=0):
@@ -82,32 +60,32 @@ def test_fused_attention_matches_eager_to_second_order():
         assert torch.allclose(g_, w_, atol=1e-11)
 
 
-def test_none_cotangents_become_expanded_zero_rows():
+def test_none_cotangents_become_expanded_zero_rows(calls):
     q, k, v, do, gq, gk, gv = _inputs(seed=1)
     qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
     o = ops.fused_attention(qq, kk, vv)
     dq, dk, dv = torch.autograd.grad(o, (qq, kk, vv), do, create_graph=True)
-    PLANT["calls"].clear()
+    calls.clear()
     hq, hk = torch.autograd.grad((dq * gq).sum(), (qq, kk))  # gk, gv are None in the bwd node's backward
-    bb = [c for c in PLANT["calls"] if isinstance(c, tuple)]
+    bb = [c for c in calls if isinstance(c, tuple)]
     assert len(bb) == 1
-    _, sq, sk, sv = bb[0]
+    _, (sq, sk, sv) = bb[0]
     assert sk == (0, 0, 0, 1) and sv == (0, 0, 0, 1)  # one zero row expanded, no L x D memory
     z = torch.zeros_like(q)
     want = oracle.autograd_bwd_bwd(q, k, v, do, gq, z, z)
     assert torch.allclose(hq, want[0], atol=1e-11) and torch.allclose(hk, want[1], atol=1e-11)
 
 
-def test_call_sequence_of_a_graded_microstep():
+def test_call_sequence_of_a_graded_microstep(calls):
     """fwd x1; first backward x1 (create_graph); outer backward: bwd_bwd x1 and attn_bwd once more (ops.py:131-185)."""
     q, k, v, do, gq, gk, gv = _inputs(seed=2)
     x = q.clone().requires_grad_(True)
     w = torch.randn(8, 8, dtype=F64, requires_grad=True)
-    PLANT["calls"].clear()
+    calls.clear()
     o = ops.fused_attention(x @ w, k, v)
     (g,) = torch.autograd.grad(o.sum(), x, create_graph=True)
     (g * gq).sum().backward()
-    names = [c if isinstance(c, str) else c[0] for c in PLANT["calls"]]
+    names = [c if isinstance(c, str) else c[0] for c in calls]
     assert names.count("fwd") == 1 and names.count("bwd") == 2 and names.count("bwd_bwd") == 1
     assert w.grad is not None
 
@@ -193,15 +171,16 @@ def test_rows_keeps_aligned_views_and_copies_others():
     assert ops._rows(odd64) is odd64
 
 
-def test_loader_modes(monkeypatch):
-    monkeypatch.setenv("EBR_FUSED_ATTN_IMPL", "reference")
-    with pytest.raises(RuntimeError, match="no dense"):
-        loader.hip_library()
+def test_loader_modes_and_routing(monkeypatch):
     monkeypatch.setenv("EBR_FUSED_ATTN_IMPL", "bogus")
     with pytest.raises(ValueError):
         loader.mode()
-    monkeypatch.setenv("EBR_FUSED_ATTN_IMPL", "triton")
-    assert loader.mode() == "triton"
+    for m in ("auto", "hip", "triton"):
+        monkeypatch.setenv("EBR_FUSED_ATTN_IMPL", m)
+        assert ops.route("cpu") == "reference" and ops.route("cuda") == "hip"
+    monkeypatch.setenv("EBR_FUSED_ATTN_IMPL", "reference")
+    assert ops.route("cpu") == "reference" and ops.route("cuda") == "reference"
+    assert ops.implementation("cuda") == "reference"
     from ebr_amd import _capi
 
     monkeypatch.setattr(_capi, "_LIB", None)
@@ -209,16 +188,103 @@ def test_loader_modes(monkeypatch):
     monkeypatch.setenv("EBR_FUSED_ATTN_IMPL", "auto")
     with pytest.raises(RuntimeError, match="unavailable"):
         loader.hip_library()
-    assert ops.implementation("cpu") == "none"
-    assert ops.implementation("cuda") == "none"
+    assert ops.implementation("cpu") == "reference"
+    assert ops.implementation("cuda") == "unavailable"  # a GPU call would raise, never fall back
+
+
+def test_cpu_tensors_run_the_dense_path_and_equal_the_oracle():
+    """fused_attention's ops on CPU tensors (reference ops.py:68-70) against the oracle, in every dtype, with views."""
+    for dt, tol in ((F64, 1e-13), (torch.float32, 1e-6), (torch.bfloat16, 1e-2), (torch.float16, 2e-3)):
+        q, k, v, do, gq, gk, gv = oracle.make_inputs(2, 3, 21, 24, dtype=dt, seed=11, qkv_scale=0.5)
+        qv = torch.cat([q, q], dim=-1)[..., :24]  # a strided view
+        s = 24**-0.5
+        o, lse = ops.attn_fwd(qv, k, v, s)
+        assert lse.dtype == ops.lse_dtype_for(q) and o.dtype == dt and o.is_contiguous()
+        ref_o, ref_lse = oracle.attn_fwd(q, k, v, s)
+        assert oracle.rel_err(o, ref_o) <= tol and oracle.rel_err(lse, ref_lse) <= tol
+        d = ops.attn_bwd(qv, k, v, o, lse, do, s)
+        for got, ref in zip(d, oracle.attn_bwd(q, k, v, o, lse, do, s)):
+            assert got.dtype == dt and oracle.rel_err(got, ref) <= tol
+        h = ops.attn_bwd_bwd(qv, k, v, o, lse, do, d[0], gq, gk, gv, s)
+        for got, ref in zip(h, oracle.attn_bwd_bwd(q, k, v, o, lse, do, None, gq, gk, gv, s)):
+            assert got.dtype == dt and oracle.rel_err(got, ref) <= tol
+
+
+def test_dense_path_groups_long_sequences_without_changing_values(monkeypatch):
+    q, k, v, do, gq, gk, gv = _inputs(B=2, H=3, L=33, D=8, seed=12)
+    s = 0.4
+    whole = [ops.attn_fwd(q, k, v, s)]
+    monkeypatch.setattr(dense, "_GROUP_ELEMS", 33 * 33 * 2)  # two (b, h) slices per group: 3 groups
+    grouped = [ops.attn_fwd(q, k, v, s)]
+    for a, b in zip(whole[0], grouped[0]):
+        assert torch.equal(a, b)
+    o, lse = whole[0]
+    h = ops.attn_bwd_bwd(q, k, v, o, lse, do, do, gq, gk, gv, s)
+    for got, ref in zip(h, oracle.attn_bwd_bwd(q, k, v, o, lse, do, None, gq, gk, gv, s)):
+        assert oracle.rel_err(got, ref) <= 1e-13
+
+
+def test_kernel_head_dims_pad_to_the_row_vector():
+    assert ops.kernel_head_dim(torch.bfloat16, 64) == 64 and ops.kernel_head_dim(torch.bfloat16, 20) == 24
+    assert ops.kernel_head_dim(torch.float16, 1) == 8 and ops.kernel_head_dim(torch.float32, 36) == 36
+    assert ops.kernel_head_dim(torch.float32, 37) == 40 and ops.kernel_head_dim(F64, 37) == 37
+    assert ops.kernel_head_dim(torch.bfloat16, 121) == 128
+    with pytest.raises(ValueError):
+        ops.kernel_head_dim(torch.bfloat16, 129)
+
+
+def test_zero_head_columns_change_nothing():
+    """The padding identity the GPU path relies on, on the oracle: zero columns appended to q, k, v, dO and the
+    cotangents leave every score unchanged and give zero output columns."""
+    q, k, v, do, gq, gk, gv = _inputs(B=1, H=2, L=7, D=5, seed=13)
+    s = 5**-0.5
+    pad = lambda t: torch.nn.functional.pad(t, (0, 3))  # noqa: E731
+    o, lse = oracle.attn_fwd(q, k, v, s)
+    op, lsep = oracle.attn_fwd(pad(q), pad(k), pad(v), s)
+    assert torch.allclose(op[..., :5], o, atol=1e-15) and op[..., 5:].abs().max() == 0
+    assert torch.allclose(lsep, lse, atol=1e-15)
+    h = oracle.attn_bwd_bwd(q, k, v, o, lse, do, None, gq, gk, gv, s)
+    hp = oracle.attn_bwd_bwd(*(pad(t) for t in (q, k, v)), pad(o), lse, pad(do), None,
+                             *(pad(t) for t in (gq, gk, gv)), s)
+    for a, b in zip(h, hp):
+        assert torch.allclose(b[..., :5], a, atol=1e-14) and b[..., 5:].abs().max() == 0
+
+
+class _PlantedBwd(torch.autograd.Function):
+    """Oracle first derivative whose own derivative has hQ 10% too small: a backend with a planted mistake."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, o, lse, do):
+        ctx.save_for_backward(q, k, v, o, lse, do)
+        return oracle.attn_bwd(q, k, v, o, lse, do, q.shape[-1] ** -0.5)
+
+    @staticmethod
+    def backward(ctx, gq, gk, gv):
+        q, k, v, o, lse, do = ctx.saved_tensors
+        z = torch.zeros_like(q)
+        gq, gk, gv = (z if g is None else g for g in (gq, gk, gv))
+        hq, hk, hv, hdo = oracle.attn_bwd_bwd(q, k, v, o, lse, do, None, gq, gk, gv, q.shape[-1] ** -0.5)
+        return 0.9 * hq, hk, hv, None, None, hdo
+
+
+class _PlantedAttn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v):
+        o, lse = oracle.attn_fwd(q, k, v, q.shape[-1] ** -0.5)
+        ctx.save_for_backward(q, k, v, o, lse)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        return _PlantedBwd.apply(q, k, v, o, lse, do)
 
 
 def test_verify_second_order_passes_and_catches_planted_mistake():
-    backend = att.get_backend("fused")
-    att.verify_second_order(backend, device=torch.device("cpu"))
-    PLANT["bwd_bwd_scale"] = 0.9  # hQ off by 10%
-    with pytest.raises(att.SecondOrderUnsafeError, match="does NOT carry second order"):
-        att.verify_second_order(backend, device=torch.device("cpu"))
+    att.verify_second_order(att.get_backend("fused"), device=torch.device("cpu"))
+    planted = att.AttentionBackend("planted", _PlantedAttn.apply, True)
+    with pytest.raises(att.SecondOrderUnsafeError, match="d2E/dz2"):
+        att.verify_second_order(planted, device=torch.device("cpu"))
 
 
 def test_verify_second_order_rejects_backend_without_second_derivative():
@@ -286,10 +352,10 @@ def test_energy_attention_fused_equals_math_on_cpu():
         assert torch.allclose(a, b, atol=1e-10)
 
 
-def test_hip_ops_have_no_cpu_kernel_in_the_package():
-    """The package registers the ops for the HIP device only; this module's CPU kernel is a test double."""
+def test_package_does_not_import_the_oracle():
+    """The dense path is the package's own code; the oracle stays test infrastructure."""
     import inspect
 
-    src = inspect.getsource(ops)
-    assert 'device_types="cuda"' in src and "oracle" not in src
+    for mod in (ops, dense, loader, att):
+        assert "oracle" not in inspect.getsource(mod).replace("oracle/", "")
     assert os.path.basename(ops.__file__) == "ops.py"
