@@ -1,18 +1,21 @@
 """Benchmark of the gfx950 fused second-order attention (BASELINE metric: attention fwd + bwd + bwd_bwd TFLOP/s and %
-of the bf16 MFMA peak, on one GPU).
+of the bf16 MFMA peak, on one GPU; EBR train steps/s).
 
 A step is one pass of the hot path over one batch: attn_fwd -> attn_bwd -> attn_bwd_bwd through the ebr_fused ops
 (the calls an EBR graded microstep makes), on synthetic inputs of the BASELINE configuration already resident in HBM.
 Default workload: config 1 (Sudoku, bf16, B=768 H=8 L=81 D=64). Prints one JSON line.
 
-Timing: W untimed warm-up steps, then K steps bracketed by torch.cuda.synchronize(), timed with HIP events on the
-stream the kernels run on (torch's current stream). Steps rotate over enough input sets that their inputs alone
-exceed 512 MB, twice the 256 MB MALL, so a step's inputs have left the last-level cache since they were last read
-(cold-cache timing). The dominant kernel (the backward of the backward)
-is also timed alone through the C ABI with preallocated outputs, for the roofline entry.
+Timing: a settle phase of at least 500 ms of back-to-back steps (whatever --warmup says: the GPU's clock needs tens of
+milliseconds of load to settle), then W untimed warm-up steps, then K steps bracketed by torch.cuda.synchronize(),
+timed with HIP events on the stream the kernels run on (torch's current stream); per-phase times are the median of
+per-step events. Steps rotate over enough input sets that their inputs alone exceed 512 MB, twice the 256 MB MALL, so
+a step's inputs have left the last-level cache since they were last read (cold-cache timing). The dominant kernel
+(the backward of the backward) is also timed alone through the C ABI with preallocated outputs, for the roofline
+entry. Further legs, each timed the same way: Maze (config 2), config 4's attention shape (fwd + bwd), the
+multi-solution shapes (D = 128), and the EBR training step (config 3) and inference descent (config 4).
 
-cpu_baseline: the CPU oracle (the build's restatement of the reference's eager path) timed on this host's cores on a
-bounded sample of the same workload, reported in the same unit.
+cpu_baseline: the CPU oracle (the build's restatement of the reference's eager path) on this host's cores, each phase
+timed alone (median of 5 after a warm-up) over every slice of the workload, reported in the same unit.
 """
 
 from __future__ import annotations
@@ -68,51 +71,76 @@ def make_sets(cfg: dict, dev: torch.device, nsets: int):
     return sets
 
 
-def step(inp, scale):
+def step(inp, scale, phases=PHASES):
+    """One pass of the hot path over one input set: the ops an EBR graded microstep calls (fwd, bwd, bwd_bwd), or
+    the first ``len(phases)`` of them (an inference descent step calls fwd and bwd only)."""
     q, k, v, do, gq, gk, gv = inp
     o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
-    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
-    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
-    return o, lse, dq
+    if "bwd" in phases:
+        dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
+        if "bwd_bwd" in phases:
+            torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
+    return o
 
 
-def time_steps(sets, scale, steps: int, warmup: int):
-    """Whole-step time and per-phase event times (ms) over ``steps`` steps.
+SETTLE_MS = 500.0  # back-to-back steps before any timed loop: the GPU's clock takes tens of ms of load to settle
+
+
+def settle(sets, scale, phases=PHASES, ms: float = SETTLE_MS):
+    """Run whole steps back to back for at least ``ms`` milliseconds of wall time (independent of --warmup), so the
+    timed loop starts at the clock the GPU holds under sustained load. Returns (steps run, milliseconds)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            step(sets[n % len(sets)], scale, phases)
+            n += 1
+        torch.cuda.synchronize()
+    return n, (time.perf_counter() - t0) * 1e3
+
+
+def time_steps(sets, scale, steps: int, warmup: int, phases=PHASES):
+    """Whole-step time (ms, mean over ``steps``) and per-phase event times (ms: median and mean over ``steps``).
 
     The step time comes from a loop with events only around all ``steps`` steps; the phases from a second loop of
     the same steps with an event between the ops (those events are measurement, not workload, so they stay out of
-    the step time). The warm-up steps run first: the GPU's clock takes a few tens of milliseconds of load to settle.
-    """
+    the step time). ``warmup`` untimed steps run first."""
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     for i in range(warmup):
-        step(sets[i % len(sets)], scale)
+        step(sets[i % len(sets)], scale, phases)
     torch.cuda.synchronize()
     t0, t1 = ev(), ev()
     t0.record()
     for i in range(steps):
-        step(sets[i % len(sets)], scale)
+        step(sets[i % len(sets)], scale, phases)
     t1.record()
     torch.cuda.synchronize()
     total = t0.elapsed_time(t1)
-    marks = [[ev() for _ in range(4)] for _ in range(steps)]
+    marks = [[ev() for _ in range(len(phases) + 1)] for _ in range(steps)]
     for i in range(steps):
         q, k, v, do, gq, gk, gv = sets[i % len(sets)]
         m = marks[i]
         m[0].record()
         o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
         m[1].record()
-        dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
-        m[2].record()
-        torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
-        m[3].record()
+        if "bwd" in phases:
+            dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
+            m[2].record()
+        if "bwd_bwd" in phases:
+            torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
+            m[3].record()
     torch.cuda.synchronize()
-    phase = {p: sum(m[j].elapsed_time(m[j + 1]) for m in marks) / steps for j, p in enumerate(PHASES)}
-    return total / steps, phase
+    per = {p: [m[j].elapsed_time(m[j + 1]) for m in marks] for j, p in enumerate(phases)}
+    median = {p: statistics.median(t) for p, t in per.items()}
+    mean = {p: sum(t) / len(t) for p, t in per.items()}
+    return total / steps, median, mean
 
 
-def time_kernel_bwd_bwd(cfg, sets, scale, reps: int):
-    """Average duration (ms) of one ebr_attn_bwd_bwd launch through the C ABI, outputs preallocated, launched
-    back-to-back on torch's current stream over rotating input sets; HIP events on that stream."""
+def time_kernel(cfg, sets, scale, reps: int, op: str = "bwd_bwd"):
+    """Average duration (ms) of one ``ebr_attn_<op>`` launch (op: "bwd" or "bwd_bwd") through the C ABI, outputs and
+    scratch preallocated, launched back-to-back on torch's current stream over rotating input sets; HIP events on
+    that stream."""
     lib = _capi.load()
     B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
     dev = sets[0][0].device
@@ -122,7 +150,8 @@ def time_kernel_bwd_bwd(cfg, sets, scale, reps: int):
         o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
         outs = [torch.empty_like(q) for _ in range(4)]
         prepared.append((inp, o, lse, outs))
-    nbytes = int(lib.ebr_attn_scratch_bytes(_capi.OP_BWD_BWD, B, H, L, D))
+    code = _capi.OP_BWD_BWD if op == "bwd_bwd" else _capi.OP_BWD
+    nbytes = int(lib.ebr_attn_scratch_bytes(code, B, H, L, D))
     scratch = torch.empty(max(1, nbytes // 4), device=dev, dtype=torch.float32) if nbytes else None
     sp = scratch.data_ptr() if scratch is not None else 0
     stream = torch.cuda.current_stream(dev)
@@ -130,14 +159,22 @@ def time_kernel_bwd_bwd(cfg, sets, scale, reps: int):
 
     def launch(i):
         (q, k, v, do, gq, gk, gv), o, lse, outs = prepared[i % len(prepared)]
-        rc = lib.ebr_attn_bwd_bwd(
-            DT_CODE[dt], B, H, L, D, ctypes.c_float(scale),
-            q.data_ptr(), s3(q), k.data_ptr(), s3(k), v.data_ptr(), s3(v), o.data_ptr(), lse.data_ptr(),
-            do.data_ptr(), s3(do), gq.data_ptr(), s3(gq), gk.data_ptr(), s3(gk), gv.data_ptr(), s3(gv),
-            outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(), outs[3].data_ptr(), sp,
-            ctypes.c_void_p(stream.cuda_stream),
-        )  # fmt: skip
-        _capi.check(rc, "ebr_attn_bwd_bwd")
+        if op == "bwd_bwd":
+            rc = lib.ebr_attn_bwd_bwd(
+                DT_CODE[dt], B, H, L, D, ctypes.c_float(scale),
+                q.data_ptr(), s3(q), k.data_ptr(), s3(k), v.data_ptr(), s3(v), o.data_ptr(), lse.data_ptr(),
+                do.data_ptr(), s3(do), gq.data_ptr(), s3(gq), gk.data_ptr(), s3(gk), gv.data_ptr(), s3(gv),
+                outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(), outs[3].data_ptr(), sp,
+                ctypes.c_void_p(stream.cuda_stream),
+            )  # fmt: skip
+        else:
+            rc = lib.ebr_attn_bwd(
+                DT_CODE[dt], B, H, L, D, ctypes.c_float(scale),
+                q.data_ptr(), s3(q), k.data_ptr(), s3(k), v.data_ptr(), s3(v), o.data_ptr(), lse.data_ptr(),
+                do.data_ptr(), s3(do), outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(), sp,
+                ctypes.c_void_p(stream.cuda_stream),
+            )  # fmt: skip
+        _capi.check(rc, f"ebr_attn_{op}")
 
     for i in range(3):
         launch(i)
@@ -177,66 +214,67 @@ def spot_check(sample, scale) -> float:
     return max(oracle.rel_err(g, r) for g, r in zip(got, [o_r, lse_r, *d_r, *h_r]))
 
 
-def cpu_baseline(cfg, scale, budget_s: float):
-    """The CPU oracle (eager dense path) on the first ``nbh`` (b, h) slices of the workload; fwd + bwd + bwd_bwd
-    timed together, median of 3 after one warm-up; nbh chosen so one pass takes about budget_s / 4."""
+def cpu_baseline(cfg, scale, nbh: int = 0, reps: int = 5):
+    """The CPU oracle (eager dense path) on the first ``nbh`` (b, h) slices of the workload (0: all of them): fwd,
+    bwd and bwd_bwd each timed on their own, median of ``reps`` after one warm-up (the BASELINE CPU plan); the value
+    is the three phases' flops over the sum of their medians."""
     import oracle
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
-
-    def inputs(nbh):
-        bb = max(1, nbh // H)
-        return oracle.make_inputs(bb, H, L, D, dtype=dt, seed=0, qkv_scale=cfg["qkv_scale"]), bb
-
+    nbh = B * H if nbh <= 0 else min(nbh, B * H)
+    bb = max(1, nbh // H)
+    q, k, v, do, gq, gk, gv = oracle.make_inputs(bb, H, L, D, dtype=dt, seed=0, qkv_scale=cfg["qkv_scale"])
     chunk = max(1, (1 << 22) // (L * L))  # (b, h) slices per dense pass: bounds the L x L temporaries
-
-    def one(inp):
-        q, k, v, do, gq, gk, gv = inp
-        o, lse = oracle.attn_fwd(q, k, v, scale, chunk=chunk)
-        dq, dk, dv = oracle.attn_bwd(q, k, v, o, lse, do, scale, chunk=chunk)
-        oracle.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale, chunk=chunk)
-
-    target = budget_s / 4.0
-    nbh = min(B * H, 64 * H)
-    while True:
-        inp, bb = inputs(nbh)
-        t = time.perf_counter()
-        one(inp)  # also the warm-up of the final size
-        probe = time.perf_counter() - t
-        if bb * H >= B * H or probe >= target / 2:
-            break
-        nbh = int(min(B * H, nbh * max(2.0, target / max(probe, 1e-3))))
-    times = []
-    for _ in range(3):
-        t = time.perf_counter()
-        one(inp)
-        times.append(time.perf_counter() - t)
-    sec = statistics.median(times)
+    o, lse = oracle.attn_fwd(q, k, v, scale, chunk=chunk)
+    dq, _, _ = oracle.attn_bwd(q, k, v, o, lse, do, scale, chunk=chunk)
+    calls = {
+        "fwd": lambda: oracle.attn_fwd(q, k, v, scale, chunk=chunk),
+        "bwd": lambda: oracle.attn_bwd(q, k, v, o, lse, do, scale, chunk=chunk),
+        "bwd_bwd": lambda: oracle.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale, chunk=chunk),
+    }
+    phase_s = {}
+    for p, fn in calls.items():
+        fn()  # warm-up
+        times = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+        phase_s[p] = statistics.median(times)
+    sec = sum(phase_s.values())
     flops = sum(roofline.phase_flops(p, bb, H, L, D) for p in PHASES)
     return {
         "value": round(flops / sec / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"CPU oracle (eager dense restatement of models/fused_attn/reference.py), fwd+bwd+bwd_bwd on "
-        f"{bb * H} of {B * H} (b,h) slices (B={bb}, H={H}, L={L}, D={D}, {DT_NAME[dt]} inputs, fp32 compute), "
-        f"median of 3 passes of {sec:.3f} s after 1 warm-up, torch threads={cores}",
-        "seconds_per_pass": round(sec, 4),
-        "cpu_model": _cpu_model(),
+        "sample": f"CPU oracle (eager dense restatement of models/fused_attn/reference.py) on {bb * H} of {B * H} "
+        f"(b,h) slices (B={bb}, H={H}, L={L}, D={D}, {DT_NAME[dt]} inputs, fp32 compute): fwd, bwd and bwd_bwd "
+        f"each timed alone, median of {reps} after 1 warm-up, torch threads={cores}",
+        "phase_seconds": {p: round(t, 4) for p, t in phase_s.items()},
+        "phase_tflops": {p: round(roofline.phase_flops(p, bb, H, L, D) / t / 1e12, 4) for p, t in phase_s.items()},
+        "cpu": cpu_info(),
     }
 
 
-def _cpu_model() -> str:
+def cpu_info() -> dict:
+    """The host CPU's model name, its logical CPU count, and which of the ISA extensions that matter to the eager
+    baseline's bf16 / fp32 GEMMs it reports."""
+    model, flags = "unknown", set()
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
     except OSError:
         pass
-    return "unknown"
+    isa = ["avx2", "fma", "avx512f", "avx512_bf16", "avx512_vnni", "avx512_fp16", "amx_tile", "amx_bf16"]
+    return {"model": model, "logical_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "isa": {f: f in flags for f in isa}}
 
 
 def bb_kernel_name(cfg: dict) -> str:
@@ -255,10 +293,31 @@ def bb_kernel_name(cfg: dict) -> str:
     return f"k_bb_fused<{DT_NAME[dt]}>"
 
 
-def measured_traffic(config: int, kname: str):
+def bwd_kernel_name(cfg: dict) -> str:
+    """The kernel(s) ebr_attn_bwd dispatches for this workload (mirrors BwdLaunch::run in ebr_attn.hip)."""
+    L, D, dt = cfg["L"], cfg["D"], cfg["dtype"]
+    if L > 128:
+        if dt != torch.float32 and D in (32, 64):
+            nw = 7 if cfg["B"] * cfg["H"] * -(-L // 112) >= 1024 else 4
+            return f"k_bwd_long_row<{DT_NAME[dt]}, {D}, {nw}> + k_bwd_long_col<{DT_NAME[dt]}, {D}, {nw}>"
+        return f"k_bwd_row<{DT_NAME[dt]}, {D}> + k_bwd_col<{DT_NAME[dt]}, {D}>"
+    if dt != torch.float32 and D in (32, 64, 128):
+        nch = (L + 31) // 32
+        kern = "k_bwd_pipe" if D <= 64 and nch <= 3 else "k_bwd_res"
+        return f"{kern}<{DT_NAME[dt]}, {D}, {nch}>"
+    return f"k_bwd_fused<{DT_NAME[dt]}>"
+
+
+TRAFFIC_FILES = {"sudoku_attn_bf16": "sudoku_bf16", "maze_attn_bf16": "maze_bf16",
+                 "config4_attn_bf16": "config4_attn_bf16"}
+
+
+def measured_traffic(workload: str, kname: str):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
     (profiles/<workload>_traffic.json, calibrated against a 256 MiB copy), or None when no summary matches."""
-    name = {0: "nqueens8_fp32", 1: "sudoku_bf16", 2: "maze_bf16"}.get(config)
+    name = TRAFFIC_FILES.get(workload)
+    if name is None:
+        return None, None
     path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
     try:
         with open(path) as f:
@@ -272,6 +331,72 @@ def measured_traffic(config: int, kname: str):
             return None, None
         total += k["fetch_bytes"] + k["write_bytes"]
     return round(total), os.path.relpath(path, ROOT)
+
+
+def attn_leg(cfg: dict, steps: int, warmup: int, phases=PHASES, kernel_reps: int = 20, nsets: int = 0,
+             settle_ms: float = SETTLE_MS, sets=None) -> dict:
+    """One attention workload: the settle phase, the step loop (``phases`` of fwd -> bwd -> bwd_bwd), each phase's
+    median event time, TFLOP/s, % of the bf16 peak, GB/s of its algorithmic bytes and % of its roofline, and the
+    dominant kernel (the last phase) timed alone through the C ABI for the roofline entry."""
+    dev = torch.device("cuda", 0)
+    B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
+    scale = D**-0.5
+    es = torch.tensor([], dtype=dt).element_size()
+    dname = DT_NAME[dt]
+    if sets is None:
+        nsets = nsets if nsets > 0 else cold_sets(cfg)
+        sets = make_sets(cfg, dev, nsets)
+    log(f"workload {cfg['name']} B={B} H={H} L={L} D={D} {dname}: {len(sets)} input sets, phases {'+'.join(phases)}")
+    n_settle, ms_settle = settle(sets, scale, phases, settle_ms)
+    ms_step, med, mean = time_steps(sets, scale, steps, warmup, phases)
+    log(f"{cfg['name']}: settle {n_settle} steps / {ms_settle:.0f} ms; ms/step {ms_step:.4f}; phase medians "
+        + " ".join(f"{p}={med[p]:.4f}ms" for p in phases))
+    dom = phases[-1]
+    k_ms = time_kernel(cfg, sets, scale, kernel_reps, dom)
+    log(f"{cfg['name']}: {dom} kernel (C ABI, back-to-back) {k_ms:.4f} ms")
+    flops_step = sum(roofline.phase_flops(p, B, H, L, D) for p in phases)
+    t_roof = sum(roofline.roof_time_s(p, B, H, L, D, es, dname) for p in phases)
+    per_phase = {}
+    for p in phases:
+        f, by, t = roofline.phase_flops(p, B, H, L, D), roofline.phase_bytes(p, B, H, L, D, es), med[p] * 1e-3
+        per_phase[p] = {
+            "ms": round(med[p], 4),
+            "ms_mean": round(mean[p], 4),
+            "tflops": round(f / t / 1e12, 2),
+            "pct_bf16_peak": round(100 * f / t / 1e12 / roofline.PEAK_BF16_TFLOPS, 2),
+            "gbs": round(by / t / 1e9, 1),
+            "pct_roofline": round(100 * roofline.roof_time_s(p, B, H, L, D, es, dname) / t, 1),
+            "bound": roofline.bound(p, B, H, L, D, es, dname),
+        }
+    by, fl = roofline.phase_bytes(dom, B, H, L, D, es), roofline.phase_flops(dom, B, H, L, D)
+    if roofline.bound(dom, B, H, L, D, es, dname) == "hbm":
+        achieved = by / (k_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": roofline.PEAK_HBM_GBS, "unit": "GB/s"}
+    else:
+        achieved = fl / (k_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": roofline.peak_tflops(dname),
+                "unit": "TFLOP/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    kname = bb_kernel_name(cfg) if dom == "bwd_bwd" else bwd_kernel_name(cfg)
+    roof["traffic"], roof["traffic_source"] = measured_traffic(cfg["name"], kname)
+    if roof["traffic"] is not None:
+        roof["traffic_vs_algorithmic"] = round(roof["traffic"] / by, 4)
+    roof["kernel"] = f"ebr_attn_{dom} ({kname})"
+    roof["kernel_ms"] = round(k_ms, 4)
+    roof["algorithmic_per_launch"] = {"bytes": by, "flops": fl}
+    tflops = flops_step / (ms_step * 1e-3) / 1e12
+    return {
+        "workload": f"{cfg['name']}: {' + '.join('attn_' + p for p in phases)}, B={B} H={H} L={L} D={D} {dname}, "
+                    "non-causal",
+        "ms_per_step": round(ms_step, 4),
+        "tflops": round(tflops, 3),
+        "pct_bf16_peak": round(100 * tflops / roofline.PEAK_BF16_TFLOPS, 2),
+        "pct_attainable_roofline": round(100 * t_roof / (ms_step * 1e-3), 1),
+        "settle_ms": round(ms_settle, 1),
+        "settle_steps": n_settle,
+        "phases": per_phase,
+        "roofline": roof,
+    }
 
 
 def pmc_target(cfg: dict, reps: int = 3) -> None:
@@ -309,7 +434,8 @@ def multi_solution_bench(steps: int, warmup: int) -> dict:
         cfg = dict(name=f"B={B} H={H} L={L} D={D}", B=B, H=H, L=L, D=D, dtype=torch.bfloat16, qkv_scale=0.125)
         sets = make_sets(cfg, dev, max(2, -(-MALL_FLUSH_BYTES // (7 * B * H * L * D * 2))))
         scale = D**-0.5
-        ms, ph = time_steps(sets, scale, steps, warmup)
+        settle(sets, scale)
+        ms, ph, _ = time_steps(sets, scale, steps, warmup)
         roof = sum(roofline.roof_time_s(p, B, H, L, D, 2, "bf16") for p in PHASES)
         flops = sum(roofline.phase_flops(p, B, H, L, D) for p in PHASES)
         out[f"L{L}"] = {"ms_per_step": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
@@ -333,11 +459,24 @@ def descent_target(reps: int = 20) -> None:
     print(json.dumps(descent_bench(reps, False, 0)), flush=True)
 
 
-def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
+def _median_ms(fn, n: int) -> float:
+    """Median over ``n`` calls of ``fn`` of the HIP-event time around each call (ms)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def ebr_train(steps: int, warmup: int, cpu_batches=(8, 16)):
     """BASELINE config 3: 2 post-norm blocks, hidden 512, 8 x 64 heads, SwiGLU x4, mean-pooled linear energy head;
     x ~ U{0..10} [384, 81]; z ~ N(0, 1) [384, 81, 512]; 16 steps z <- z - 0.1 dE/dz with create_graph; CE of a linear
-    decode head to random targets; backward; bf16. GPU: the fused (gfx950) attention. CPU: the same step with the eager
-    'math' attention on the host's cores, at batch ``cpu_sample_b``, scaled linearly to batch 384."""
+    decode head to random targets; backward; bf16. GPU: the fused (gfx950) attention, median of ``steps`` timed steps,
+    eager and graph-captured. CPU: the same step eager with the 'math' attention on the host's cores at the batch
+    sizes ``cpu_batches`` (median of 3 each after one warm-up), the per-row time of the largest scaled linearly to
+    batch 384."""
     from ebr_amd import energy as en
 
     B, L, V = 384, 81, 11
@@ -352,74 +491,74 @@ def ebr_train(steps: int, warmup: int, cpu_sample_b: int):
     x = torch.randint(0, V, (B, L), generator=g).to(dev)
     z0 = torch.randn(B, L, cfg.hidden_size, generator=g).to(dev, torch.bfloat16)
     tg = torch.randint(0, V, (B, L), generator=g).to(dev)
-    for _ in range(warmup):
-        en.train_step(model, dec, x, z0, tg)
+    last = {}
+
+    def one():
+        last["loss"] = en.train_step(model, dec, x, z0, tg)
         model.zero_grad(set_to_none=True)
         dec.zero_grad(set_to_none=True)
+
+    for _ in range(warmup):
+        one()
     torch.cuda.synchronize()
     # The long-lived objects (modules, parameters, the library) move out of the collector's view, as training loops
     # do: a full collection otherwise walks them while a step's autograd graph is alive (about 25 ms when it runs).
     gc.collect()
     gc.freeze()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        loss = en.train_step(model, dec, x, z0, tg)
-        model.zero_grad(set_to_none=True)
-        dec.zero_grad(set_to_none=True)
-    e1.record()
-    torch.cuda.synchronize()
+    ms = _median_ms(one, steps)
     gc.unfreeze()
-    ms = e0.elapsed_time(e1) / steps
+    loss = last["loss"]
     # The same step captured in a HIP graph over the same static inputs: each step is one graph launch, with no
     # Python, autograd or launch work on the host (the eager step above waits on the host for part of its time).
-    model.zero_grad(set_to_none=True)
-    dec.zero_grad(set_to_none=True)
     graph, gloss = en.graph_train_step(model, dec, x, z0, tg)
     graph.replay()
     torch.cuda.synchronize()
-    e0.record()
-    for _ in range(steps):
-        graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    gms = e0.elapsed_time(e1) / steps
+    gms = _median_ms(graph.replay, steps)
     graphed = {"steps_per_s": round(1000.0 / gms, 3), "ms_per_step": round(gms, 2), "loss": round(float(gloss), 4),
-               "loss_equals_eager": bool(torch.equal(gloss, loss))}
+               "loss_equals_eager": bool(torch.equal(gloss, loss)), "timed_steps": steps, "statistic": "median"}
     del graph
     out = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 2), "loss": round(float(loss), 4),
-           "graph": graphed,
+           "timed_steps": steps, "statistic": "median", "graph": graphed,
            "config": "B=384 L=81 hidden=512 heads=8x64 layers=2 SwiGLU x4, 16 create_graph descent steps, bf16; 2D RoPE "
                      "by the fused split/merge (the reference's Sudoku recipe), rms_norm and SwiGLU activation by the "
                      "fused block kernels, projection weight gradients as split-K GEMMs with fp32 partials; Python's "
                      "collector frozen after warm-up (gc.freeze); CPU: the same step eager (broadcast RoPE, eager "
                      "block and linear)",
            "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 2**30, 1)}
-    if cpu_sample_b > 0:
+    if cpu_batches:
         cores = len(os.sched_getaffinity(0))
         torch.set_num_threads(cores)
         ccfg = en.EnergyConfig(attn_backend="math", attn_nograd_backend="math")
         cm, cd = en.build(ccfg, torch.device("cpu"))
-        cx, cz, ct = x[:cpu_sample_b].cpu(), z0[:cpu_sample_b].cpu(), tg[:cpu_sample_b].cpu()
-        en.train_step(cm, cd, cx, cz, ct)  # warm-up (and the second-order self-test)
-        times = []
-        for _ in range(2):
-            cm.zero_grad(set_to_none=True)
-            t = time.perf_counter()
-            en.train_step(cm, cd, cx, cz, ct)
-            times.append(time.perf_counter() - t)
-        sec = min(times) * B / cpu_sample_b
+        per_batch = {}
+        for nb in cpu_batches:
+            cx, cz, ct = x[:nb].cpu(), z0[:nb].cpu(), tg[:nb].cpu()
+            en.train_step(cm, cd, cx, cz, ct)  # warm-up (and, the first time, the second-order self-test)
+            times = []
+            for _ in range(3):
+                cm.zero_grad(set_to_none=True)
+                cd.zero_grad(set_to_none=True)
+                t = time.perf_counter()
+                en.train_step(cm, cd, cx, cz, ct)
+                times.append(time.perf_counter() - t)
+            per_batch[nb] = statistics.median(times)
+        nb = max(cpu_batches)
+        sec = per_batch[nb] * B / nb
         out["cpu"] = {"steps_per_s": round(1.0 / sec, 5), "cores": cores, "kind": "port",
-                      "sample": f"the same step with the eager math attention at batch {cpu_sample_b} (of {B}), "
-                      f"best of 2 after 1 warm-up, scaled linearly to batch {B}"}
+                      "seconds_at_batch": {str(b): round(t, 3) for b, t in per_batch.items()},
+                      "sample": f"the same step eager with the math attention at batches {list(cpu_batches)} of {B} "
+                      f"(median of 3 after 1 warm-up each; the seconds per step scale with the batch as shown), the "
+                      f"batch-{nb} time scaled linearly to batch {B}", "cpu": cpu_info()}
         out["speedup_vs_cpu"] = round(out["steps_per_s"] / out["cpu"]["steps_per_s"], 1)
+        out["graph_speedup_vs_cpu"] = round(graphed["steps_per_s"] / out["cpu"]["steps_per_s"], 1)
     return out
 
 
-def ebr_infer(cpu_sample_n: int):
+def ebr_infer(cpu: bool):
     """256 inputs x 20 samples = 5120 sequences of L = 100 (10 x 10), same architecture, 64 descent
-    steps of dE/dz without a graph (fwd + bwd), lowest-energy sample per input; bf16. The CPU time runs
-    ``cpu_sample_n`` sequences for 2 steps and is scaled linearly to 5120 sequences and 64 steps."""
+    steps of dE/dz without a graph (fwd + bwd), lowest-energy sample per input; bf16. The CPU runs the same 5120
+    sequences eagerly for 2 descent steps (after a 1-step warm-up on 8 inputs), scaled linearly to 64 steps (every
+    step does the same work)."""
     from ebr_amd import energy as en
 
     N, S, L, V, STEPS = 256, 20, 100, 3, 64
@@ -442,19 +581,25 @@ def ebr_infer(cpu_sample_n: int):
     out = {"seconds": round(sec, 3), "ms_per_descent_step": round(sec / STEPS * 1e3, 2),
            "config": "5120 x L=100, 64 descent steps (fwd+bwd), bf16, argmin over 20 samples; 2D RoPE by the fused "
            "split/merge, rms_norm and SwiGLU activation by the fused block kernels; CPU: eager"}
-    if cpu_sample_n > 0:
-        torch.set_num_threads(len(os.sched_getaffinity(0)))
+    if cpu:
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
         ccfg = en.EnergyConfig(grid=(10, 10), vocab_size=V, attn_backend="math", attn_nograd_backend="math")
         cm, _ = en.build(ccfg, torch.device("cpu"))
         for p in cm.parameters():
             p.requires_grad_(False)
-        n_in = max(1, cpu_sample_n // S)
-        en.infer(cm, x[:n_in].cpu(), z0[: n_in * S].cpu(), S, steps=1)
+        xc, zc = x.cpu(), z0.cpu()
+        en.infer(cm, xc[:8], zc[: 8 * S], S, steps=1)
+        with torch.no_grad():
+            x_emb = cm.puzzle_embedding(xc.repeat_interleave(S, dim=0), zc.dtype)
         t = time.perf_counter()
-        en.infer(cm, x[:n_in].cpu(), z0[: n_in * S].cpu(), S, steps=2)
-        csec = (time.perf_counter() - t) / 2 * STEPS * (N / n_in)
+        en.descend(cm, zc, x_emb, 2, 0.1, create_graph=False)
+        c2 = time.perf_counter() - t
+        csec = c2 / 2 * STEPS
         out["cpu_seconds_extrapolated"] = round(csec, 1)
-        out["cpu_sample"] = f"{n_in * S} sequences x 2 steps, scaled linearly to 5120 sequences x 64 steps"
+        out["cpu_seconds_2_steps"] = round(c2, 2)
+        out["cpu_cores"] = cores
+        out["cpu_sample"] = "all 5120 sequences for 2 descent steps, scaled linearly to 64 steps"
         out["speedup_vs_cpu"] = round(csec / sec, 1)
     return out
 
@@ -755,7 +900,9 @@ def main() -> int:
     ap.add_argument("--no-multi", action="store_true", help="skip the multi-solution (D = 128) attention shapes")
     ap.add_argument("--no-block", action="store_true", help="skip the fused energy-block (rms_norm, SwiGLU) leg")
     ap.add_argument("--no-ebr-infer", action="store_true", help="skip the inference descent (config 4)")
-    ap.add_argument("--ebr-steps", type=int, default=3)
+    ap.add_argument("--ebr-steps", type=int, default=10)
+    ap.add_argument("--no-maze", action="store_true", help="skip the Maze (config 2) attention leg")
+    ap.add_argument("--no-config4-attn", action="store_true", help="skip config 4's attention shape (fwd + bwd)")
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
     ap.add_argument("--descent-target", action="store_true", help="run only the descent-wrapper leg (for rocprofv3)")
     ap.add_argument("--block-target", action="store_true", help="run only the energy-block leg (for rocprofv3)")
@@ -766,7 +913,6 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=0,
                     help="input sets rotated across steps (0: enough that their inputs exceed 512 MB)")
     ap.add_argument("--kernel-reps", type=int, default=20)
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work (0 = skip)")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
 
@@ -797,62 +943,21 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     B, H, L, D, dt = cfg["B"], cfg["H"], cfg["L"], cfg["D"], cfg["dtype"]
     scale = D**-0.5
-    es = torch.tensor([], dtype=dt).element_size()
     dname = DT_NAME[dt]
-    nsets = args.sets if args.sets > 0 else cold_sets(cfg)
-    log(f"workload {cfg['name']} B={B} H={H} L={L} D={D} {dname}; {nsets} input sets")
-    sets = make_sets(cfg, dev, nsets)
-
+    sets = make_sets(cfg, dev, args.sets if args.sets > 0 else cold_sets(cfg))
     sample = gpu_sample(cfg, sets, scale)
-
-    torch.cuda.synchronize()
-    ms_step, phase_ms = time_steps(sets, scale, args.steps, args.warmup)
-    log(f"ms/step {ms_step:.4f}; phases " + " ".join(f"{p}={phase_ms[p]:.4f}ms" for p in PHASES))
-    k_ms = time_kernel_bwd_bwd(cfg, sets, scale, args.kernel_reps)
-    log(f"bwd_bwd kernel (C ABI, back-to-back) {k_ms:.4f} ms")
-
-    flops_step = sum(roofline.phase_flops(p, B, H, L, D) for p in PHASES)
-    tflops = flops_step / (ms_step * 1e-3) / 1e12
-    peak = roofline.peak_tflops(dname)
-    t_roof = sum(roofline.roof_time_s(p, B, H, L, D, es, dname) for p in PHASES)
-    phases = {}
-    for p in PHASES:
-        f = roofline.phase_flops(p, B, H, L, D)
-        by = roofline.phase_bytes(p, B, H, L, D, es)
-        t = phase_ms[p] * 1e-3
-        phases[p] = {
-            "ms": round(phase_ms[p], 4),
-            "tflops": round(f / t / 1e12, 2),
-            "pct_bf16_peak": round(100 * f / t / 1e12 / roofline.PEAK_BF16_TFLOPS, 2),
-            "gbs": round(by / t / 1e9, 1),
-            "pct_roofline": round(100 * roofline.roof_time_s(p, B, H, L, D, es, dname) / t, 1),
-        }
-
-    hbm_bound = roofline.phase_bytes("bwd_bwd", B, H, L, D, es) / (roofline.PEAK_HBM_GBS * 1e9) >= roofline.phase_flops(
-        "bwd_bwd", B, H, L, D
-    ) / (peak * 1e12)
-    if hbm_bound:
-        achieved = roofline.phase_bytes("bwd_bwd", B, H, L, D, es) / (k_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": roofline.PEAK_HBM_GBS, "unit": "GB/s"}
-    else:
-        achieved = roofline.phase_flops("bwd_bwd", B, H, L, D) / (k_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s"}
-    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    kname = bb_kernel_name(cfg)
-    roof["traffic"], roof["traffic_source"] = measured_traffic(args.config, kname)
-    if roof["traffic"] is not None:
-        roof["traffic_vs_algorithmic"] = round(roof["traffic"] / roofline.phase_bytes("bwd_bwd", B, H, L, D, es), 4)
-    roof["kernel"] = f"ebr_attn_bwd_bwd ({kname})"
-    roof["kernel_ms"] = round(k_ms, 4)
+    head = attn_leg(cfg, args.steps, args.warmup, PHASES, args.kernel_reps, sets=sets)
+    del sets
+    torch.cuda.empty_cache()
 
     out = {
         "metric": METRIC,
-        "value": round(tflops, 3),
+        "value": head["tflops"],
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -866,21 +971,34 @@ def main() -> int:
             "D": D,
             "parallelism": "single GPU",
         },
-        "pct_bf16_peak": round(100 * tflops / roofline.PEAK_BF16_TFLOPS, 2),
-        "pct_attainable_roofline": round(100 * t_roof / (ms_step * 1e-3), 1),
-        "phases": phases,
-        "roofline": roof,
+        "pct_bf16_peak": head["pct_bf16_peak"],
+        "pct_attainable_roofline": head["pct_attainable_roofline"],
+        "settle_ms": head["settle_ms"],
+        "settle_steps": head["settle_steps"],
+        "phases": head["phases"],
+        "roofline": head["roofline"],
     }
-    if not args.no_cpu and args.cpu_budget > 0:
-        log("timing the CPU oracle baseline")
-        cb = cpu_baseline(cfg, scale, args.cpu_budget)
+    if not args.no_cpu:
+        log("timing the CPU oracle baseline (every slice of the workload, each phase alone)")
+        cb = cpu_baseline(cfg, scale)
         out["cpu_baseline"] = cb
-        out["speedup_vs_cpu"] = round(tflops / cb["value"], 1) if cb["value"] > 0 else None
+        out["speedup_vs_cpu"] = round(head["tflops"] / cb["value"], 1) if cb["value"] > 0 else None
         err = spot_check(sample, scale)
         log(f"spot-check max rel err vs CPU oracle on 16 slices: {err:.3e}")
         out["parity_max_rel_err"] = float(f"{err:.3e}")
     else:
         out["cpu_baseline"] = None
+    if not args.no_maze and args.config != 2:
+        out["maze"] = attn_leg(CONFIGS[2], max(10, args.steps // 5), 3, PHASES, args.kernel_reps)
+        if not args.no_cpu:
+            out["maze"]["cpu_baseline"] = cpu_baseline(CONFIGS[2], 64**-0.5, nbh=32)
+        log(f"maze: {out['maze']}")
+        torch.cuda.empty_cache()
+    if not args.no_config4_attn:
+        out["config4_attn"] = attn_leg(CONFIGS[4], max(10, args.steps // 5), 3, ("fwd", "bwd"), args.kernel_reps,
+                                       nsets=2)
+        log(f"config4_attn: {out['config4_attn']}")
+        torch.cuda.empty_cache()
     if not args.no_rope:
         log("fused RoPE split / merge")
         out["rope"] = rope_bench(cfg, 20, not args.no_cpu)
@@ -899,11 +1017,11 @@ def main() -> int:
         log(f"block: {out['block']}")
     if not args.no_ebr:
         log("EBR training step (config 3)")
-        out["ebr_train"] = ebr_train(args.ebr_steps, 1, 0 if args.no_cpu else 8)
+        out["ebr_train"] = ebr_train(args.ebr_steps, 2, () if args.no_cpu else (8, 16))
         log(f"EBR train: {out['ebr_train']}")
     if not args.no_ebr_infer:
         log("EBR inference descent (config 4)")
-        out["ebr_infer"] = ebr_infer(0 if args.no_cpu else 40)
+        out["ebr_infer"] = ebr_infer(not args.no_cpu)
         log(f"EBR infer: {out['ebr_infer']}")
     print(json.dumps(out), flush=True)
     return 0

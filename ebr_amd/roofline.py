@@ -37,7 +37,15 @@ def roof_time_s(phase: str, B: int, H: int, L: int, D: int, elem: int, dtype_nam
     )
 
 
+def bound(phase: str, B: int, H: int, L: int, D: int, elem: int, dtype_name: str) -> str:
+    """'hbm' when the phase's bytes take longer at peak bandwidth than its flops at peak rate, else 'mfma'."""
+    t_bytes = phase_bytes(phase, B, H, L, D, elem) / (PEAK_HBM_GBS * 1e9)
+    t_flops = phase_flops(phase, B, H, L, D) / (peak_tflops(dtype_name) * 1e12)
+    return "hbm" if t_bytes >= t_flops else "mfma"
+
+
 __all__ = [
+    "bound",
     "PEAK_BF16_TFLOPS",
     "PEAK_FP32_TFLOPS",
     "PEAK_HBM_GBS",

@@ -16,6 +16,8 @@ CONFIGS = {
     0: dict(name="nqueens8_attn_fp32", B=32, H=8, L=64, D=64, dtype=torch.float32, qkv_scale=None),
     1: dict(name="sudoku_attn_bf16", B=768, H=8, L=81, D=64, dtype=torch.bfloat16, qkv_scale=0.125),
     2: dict(name="maze_attn_bf16", B=64, H=8, L=900, D=64, dtype=torch.bfloat16, qkv_scale=0.125),
+    # config 4's attention (5120 sequences of a 10 x 10 board, 8 heads of 64); its descent calls fwd and bwd only
+    4: dict(name="config4_attn_bf16", B=5120, H=8, L=100, D=64, dtype=torch.bfloat16, qkv_scale=0.125),
 }
 
 

@@ -307,6 +307,44 @@ def test_outputs_do_not_depend_on_stale_memory(cuda):
         assert torch.equal(x, y), n
 
 
+@pytest.mark.parametrize("D", [20, 36, 72, 100])
+@pytest.mark.parametrize("L", [45, 150])
+def test_padded_head_dims_bf16(cuda, D, L):
+    """Head dims the kernels do not take natively are zero-padded to the next multiple of 8 and cut back (reference
+    triton_kernels.py:587-589 pads the same way): exact, so the usual bar holds."""
+    _case(2, 3, L, D, torch.bfloat16, cuda, seed=D * L)
+
+
+@pytest.mark.parametrize("D,dtype", [(6, torch.float32), (30, torch.float32), (20, torch.float16), (3, torch.bfloat16)])
+def test_padded_head_dims_other_dtypes(cuda, D, dtype):
+    _case(2, 2, 33, D, dtype, cuda, seed=D)
+
+
+def test_reference_mode_runs_dense_on_gpu_tensors(cuda, monkeypatch):
+    """EBR_FUSED_ATTN_IMPL=reference selects the dense torch path for GPU tensors too (reference loader.py:21-23)."""
+    from ebr_amd.fused_attn import dense
+
+    _say("EBR_FUSED_ATTN_IMPL=reference on GPU tensors")
+    monkeypatch.setenv("EBR_FUSED_ATTN_IMPL", "reference")
+    assert ops.implementation("cuda") == "reference"
+    used = []
+    monkeypatch.setattr(dense, "attn_fwd", lambda *a, f=dense.attn_fwd: used.append(1) or f(*a))
+    q, k, v, do, gq, gk, gv = _inputs(2, 2, 40, 64, torch.bfloat16, 9)
+    got = _hip_all(q, k, v, do, gq, gk, gv, 0.125, cuda)
+    assert used, "the dense path did not run"
+    ref = _oracle_all(q, k, v, do, gq, gk, gv, 0.125, o=got[0], lse=got[1])
+    _compare(got, ref, torch.bfloat16, "reference mode")
+
+
+def test_empty_batch(cuda):
+    _say("empty batch")
+    q = torch.randn(0, 2, 16, 64, device=cuda, dtype=torch.bfloat16)
+    o, lse = torch.ops.ebr_fused.attn_fwd(q, q, q, 0.125)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, q, q, o, lse, q, 0.125)
+    hs = torch.ops.ebr_fused.attn_bwd_bwd(q, q, q, o, lse, q, dq, q, q, q, 0.125)
+    assert o.shape == q.shape and lse.shape == (0, 2, 16) and all(t.shape == q.shape for t in (dq, dk, dv, *hs))
+
+
 def test_bad_arguments_raise(cuda):
     _say("argument errors")
     q = torch.randn(2, 2, 16, 64, device=cuda)
@@ -316,7 +354,7 @@ def test_bad_arguments_raise(cuda):
         torch.ops.ebr_fused.attn_fwd(q, q.half(), q, 0.125)
     with pytest.raises(TypeError):
         torch.ops.ebr_fused.attn_fwd(q.to(torch.int32), q.to(torch.int32), q.to(torch.int32), 0.125)
-    with pytest.raises(ValueError):  # D > 128
+    with pytest.raises(ValueError):  # D > 128: the kernels' registers and LDS hold at most 128 per row
         x = torch.randn(1, 1, 4, 136, device=cuda)
         torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
     assert math.isfinite(1.0)
