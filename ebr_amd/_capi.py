@@ -17,6 +17,8 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libebr_attn.so"
 DTYPE_F32, DTYPE_BF16, DTYPE_F16, DTYPE_F64 = 0, 1, 2, 3
 OP_FWD, OP_BWD, OP_BWD_BWD = 0, 1, 2
 ERR_HIP_BASE = 1000
+ERR_NOALLOC_SIZE = 6
+NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # EBR_NOALLOC_SCRATCH_BYTES
 ABI_VERSION = 2
 
 _P = ctypes.c_void_p
@@ -42,6 +44,16 @@ SIGNATURES = {
         + [_P, _I64P] * 4
         + [_P] * 4
         + [_F32P, _P],
+    ),
+    "ebr_attn_bwd_bwd_noalloc": (
+        ctypes.c_int,
+        [ctypes.c_int] * 5
+        + [ctypes.c_float]
+        + [_P, _I64P] * 3
+        + [_P, _F32P]
+        + [_P, _I64P] * 4
+        + [_P] * 4
+        + [_P],
     ),
     "ebr_attn_scratch_bytes": (ctypes.c_int64, [ctypes.c_int] * 5),
     # include/ebr_rope.h

@@ -21,7 +21,8 @@ OUT_DIR = PKG / "_lib"
 LIB_NAME = "libebr_attn.so"
 ARCH = "gfx950"
 
-SOURCES = [CSRC / "ebr_attn.hip", CSRC / "ebr_rope.hip", CSRC / "ebr_descent.hip", CSRC / "ebr_block.hip"]
+SOURCES = [CSRC / "ebr_attn.hip", CSRC / "ebr_rope.hip", CSRC / "ebr_descent.hip", CSRC / "ebr_block.hip",
+           CSRC / "ebr_noalloc.hip"]
 HEADERS = [
     CSRC / "attn_tiles.hpp",
     CSRC / "attn_resident.hpp",

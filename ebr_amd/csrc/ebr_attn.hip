@@ -1103,6 +1103,9 @@ const char* ebr_attn_error_string(int code) {
             return "row start not 16-byte aligned (8-byte for fp64) (base pointer or a B/H/L stride)";
         case EBR_ERR_NULL: return "required pointer is NULL";
         case EBR_ERR_SCRATCH: return "scratch buffer required for this shape but NULL";
+        case EBR_ERR_NOALLOC_SIZE:
+            return "shape needs more row-statistics scratch than the no-allocation entry point holds "
+                   "(EBR_NOALLOC_SCRATCH_BYTES)";
         default: break;
     }
     if (code >= EBR_ERR_HIP_BASE) return hipGetErrorString((hipError_t)(code - EBR_ERR_HIP_BASE));

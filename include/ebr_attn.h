@@ -47,6 +47,7 @@ enum {
     EBR_ERR_ALIGN = 3,       /* a pointer or stride breaks the 16-byte row alignment rule */
     EBR_ERR_NULL = 4,        /* a required pointer is NULL */
     EBR_ERR_SCRATCH = 5,     /* scratch is NULL but this shape needs one (see ebr_attn_scratch_bytes) */
+    EBR_ERR_NOALLOC_SIZE = 6, /* the shape needs more scratch than EBR_NOALLOC_SCRATCH_BYTES (no-allocation entry) */
     EBR_ERR_HIP_BASE = 1000, /* EBR_ERR_HIP_BASE + hipError_t of a failed launch */
 };
 
@@ -92,6 +93,28 @@ int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale,
                      const void* gk, const int64_t gk_str[3],
                      const void* gv, const int64_t gv_str[3],
                      void* hq, void* hk, void* hv, void* hdo, float* scratch, void* stream);
+
+/* Bytes of the library's own device scratch array behind ebr_attn_bwd_bwd_noalloc (one copy per GPU). */
+#define EBR_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+
+/* ebr_attn_bwd_bwd without the scratch argument, for callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc. It has no counterpart in the reference (whose
+ * launchers allocate their statistics buffers, models/fused_attn/triton_kernels.py:910-912). Same arguments, kernels
+ * and results as ebr_attn_bwd_bwd; the fp32 row statistics that shapes with L > 128 exchange between their two
+ * launches ([3, B, H, L], ebr_attn_scratch_bytes) live in a device array of the library, EBR_NOALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends. Shapes that need more return EBR_ERR_NOALLOC_SIZE before anything is
+ * enqueued. It calls no allocating routine. Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (concurrent streams or threads) race and must be serialised by the caller. */
+int ebr_attn_bwd_bwd_noalloc(int dtype, int B, int H, int L, int D, float scale,
+                             const void* q, const int64_t q_str[3],
+                             const void* k, const int64_t k_str[3],
+                             const void* v, const int64_t v_str[3],
+                             const void* o, const void* lse,
+                             const void* dO, const int64_t dO_str[3],
+                             const void* gq, const int64_t gq_str[3],
+                             const void* gk, const int64_t gk_str[3],
+                             const void* gv, const int64_t gv_str[3],
+                             void* hq, void* hk, void* hv, void* hdo, void* stream);
 
 /* Bytes of fp32 scratch an op needs for this shape (0 when the shape runs in one workgroup per (b, h)).
  * No reference counterpart: the Triton launchers allocate their row-statistics buffers themselves

@@ -42,8 +42,9 @@ def test_version_arch_and_error_texts():
     lib = _capi.load()
     assert lib.ebr_attn_abi_version() == _capi.ABI_VERSION == 2
     assert lib.ebr_attn_arch() == b"gfx950"
-    for code in (0, 1, 2, 3, 4, 5):
+    for code in (0, 1, 2, 3, 4, 5, 6):
         assert lib.ebr_attn_error_string(code)
+    assert b"no-allocation" in lib.ebr_attn_error_string(_capi.ERR_NOALLOC_SIZE)
     assert b"unknown" in lib.ebr_attn_error_string(77)
     assert lib.ebr_attn_error_string(_capi.ERR_HIP_BASE + 1)  # hipErrorInvalidValue text
 
@@ -135,3 +136,17 @@ def test_build_recipe_targets_gfx950_without_packed_fp32():
     assert "--offload-arch=gfx950" in flags
     i = flags.index("-packed-fp32-ops")
     assert flags[i - 1] == "-Xclang" and flags[i - 2] == "-target-feature"
+
+
+def test_noalloc_entry_rejects_shapes_beyond_its_array_before_any_hip_call():
+    """ebr_attn_bwd_bwd_noalloc checks the row-statistics size against EBR_NOALLOC_SCRATCH_BYTES first (no GPU needed:
+    nothing is looked up or enqueued), and otherwise validates arguments exactly as ebr_attn_bwd_bwd does."""
+    lib = _capi.load()
+    z = (ctypes.c_int64 * 3)(0, 0, 0)
+    tail = [16, z] * 3 + [16, 16] + [16, z] * 4 + [16, 16, 16, 16, None]
+    B, H, L, D = 600, 8, 900, 64
+    assert lib.ebr_attn_scratch_bytes(_capi.OP_BWD_BWD, B, H, L, D) > _capi.NOALLOC_SCRATCH_BYTES
+    assert lib.ebr_attn_bwd_bwd_noalloc(_capi.DTYPE_BF16, B, H, L, D, ctypes.c_float(0.125), *tail) == 6
+    assert lib.ebr_attn_bwd_bwd_noalloc(_capi.DTYPE_BF16, 0, H, L, D, ctypes.c_float(0.125), *tail) == 2  # B < 1
+    assert lib.ebr_attn_bwd_bwd_noalloc(_capi.DTYPE_BF16, 2, 2, 81, 64, ctypes.c_float(0.125), *tail[:-5],
+                                        None, 16, 16, 16, None) == 4  # hq NULL: L <= 128 needs no scratch lookup
