@@ -436,7 +436,10 @@ template <typename T, int DP, int NCH> struct BwdPipe {
     static constexpr int TB = LP * TP;            // one tile
     static constexpr int NWC = 2 * NCH;           // compute waves
     static constexpr int BUF = 4 * RB;            // K, V, Q, dO
-    static constexpr int STG = 2 * BUF + 2 * TB + 4 * LP * 4;  // byte offset of the compute waves' store areas
+    // Up to three 32-row chunks the P and dS tiles fit beside the two buffers (5 GEMM units); with four (L up to 128)
+    // they do not, and the col pass recomputes P and dS from the buffer instead (7 GEMM units, loads still overlapped).
+    static constexpr bool TILES = NCH <= 3;
+    static constexpr int STG = 2 * BUF + (TILES ? 2 * TB : 0) + 4 * LP * 4;  // byte offset of the store areas
     // two buffers | P, dS tiles | lse * log2 e (two) | rowsum(dO o O) (two) | a row-store area per compute wave
     static constexpr int SMEM = STG + NWC * RowStage16<T, DP>::BYTES;
     static constexpr int THREADS = 64 * (NWC + 1);
@@ -479,7 +482,7 @@ __device__ __forceinline__ void zero_tile_rows(unsigned char* t0, unsigned char*
     }
 }
 
-template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bwd_pipe(Args a) {
+template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NCH + 1)) void k_bwd_pipe(Args a) {
     using LY = Lay<T, DP>;
     using R = BwdPipe<T, DP, NCH>;
     constexpr int Lp = R::LP;
@@ -487,9 +490,9 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     const WaveIds w = wave_ids();
     const int L = a.L;
     const int nbh = a.B * a.H;
-    unsigned char* TPr = smem + 2 * R::BUF;  // P
-    unsigned char* TSr = TPr + R::TB;        // dS
-    float* lse_buf = reinterpret_cast<float*>(TPr + 2 * R::TB);  // [2][LP]
+    unsigned char* TPr = smem + 2 * R::BUF;  // P (when R::TILES)
+    unsigned char* TSr = TPr + R::TB;        // dS (when R::TILES)
+    float* lse_buf = reinterpret_cast<float*>(smem + 2 * R::BUF + (R::TILES ? 2 * R::TB : 0));  // [2][LP]
     float* dr_buf = lse_buf + 2 * Lp;                              // [2][LP]
     int s = blockIdx.x;
 
@@ -600,33 +603,63 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                     d0[r] = p0[r] * (d0[r] - dr);
                     d1[r] = p1[r] * (d1[r] - dr);
                 }
-                const SeqB<T> pb = make_seqb<T>(p0, p1);
                 const SeqB<T> dsb = make_seqb<T>(d0, d1);
+                if constexpr (R::TILES) {
+                    const SeqB<T> pb = make_seqb<T>(p0, p1);
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int key0 = x0 + 16 * hh + 4 * w.g;
-                    tile_store8(TPr, R::TP, own, key0, u32x2{pb.v[2 * hh], pb.v[2 * hh + 1]});
-                    tile_store8(TSr, R::TP, own, key0, u32x2{dsb.v[2 * hh], dsb.v[2 * hh + 1]});
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int key0 = x0 + 16 * hh + 4 * w.g;
+                        tile_store8(TPr, R::TP, own, key0, u32x2{pb.v[2 * hh], pb.v[2 * hh + 1]});
+                        tile_store8(TSr, R::TP, own, key0, u32x2{dsb.v[2 * hh], dsb.v[2 * hh + 1]});
+                    }
                 }
 #pragma unroll
                 for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, x0, t, lo), dsb);
             });
             store_acc_staged<T, DP>(a.out0, ((int64_t)s * L + row0) * DP, L - row0, acc, sc, stage, w.lane);
-        } else {
+        } else if constexpr (R::TILES) {
             zero_tile_rows<NCH>(TPr, TSr, nullptr, R::TP, own, w.g);
         }
         lds_barrier();  // X: tiles complete
 
-        // ---- col pass: own = keys; dV = P^T dO, dK = s dS^T Q from the tiles
+        // ---- col pass: own = keys; dV = P^T dO, dK = s dS^T Q from the tiles, or with P and dS recomputed
         if (active) {
             f32x4 ak[LY::NT], av[LY::NT];
 #pragma unroll
             for (int t = 0; t < LY::NT; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            OwnFrag<T, DP> kf, vf;
+            if constexpr (!R::TILES) {
+                own_from_lds<T, DP>(kf, Kr, row0, lo);
+                own_from_lds<T, DP>(vf, Vr, row0, lo);
+            }
             static_for<0, NCH>([&](auto cc) {
                 constexpr int C = decltype(cc)::value;
                 const int x0 = C * CH;
-                const SeqB<T> pb = tile_seqb<T>(TPr, R::TP, x0, row0, w.l16, w.g);
-                const SeqB<T> dsb = tile_seqb<T>(TSr, R::TP, x0, row0, w.l16, w.g);
+                SeqB<T> pb, dsb;
+                if constexpr (R::TILES) {
+                    pb = tile_seqb<T>(TPr, R::TP, x0, row0, w.l16, w.g);
+                    dsb = tile_seqb<T>(TSr, R::TP, x0, row0, w.l16, w.g);
+                } else {
+                    const float* dr2 = dr_buf + bsel * Lp;
+                    const f32x4 l0 = *reinterpret_cast<const f32x4*>(l2 + x0 + 4 * w.g);
+                    const f32x4 l1 = *reinterpret_cast<const f32x4*>(l2 + x0 + 16 + 4 * w.g);
+                    const f32x4 r0 = *reinterpret_cast<const f32x4*>(dr2 + x0 + 4 * w.g);
+                    const f32x4 r1 = *reinterpret_cast<const f32x4*>(dr2 + x0 + 16 + 4 * w.g);
+                    f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+                    mma_d_sw<T, DP>(p0, Qr, x0, kf, lo);
+                    mma_d_sw<T, DP>(p1, Qr, x0 + 16, kf, lo);
+                    mma_d_sw<T, DP>(d0, Or, x0, vf, lo);
+                    mma_d_sw<T, DP>(d1, Or, x0 + 16, vf, lo);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        p0[r] = fast_exp2(fmaf(p0[r], sc2, -l0[r]));  // lse = +inf on padded query rows -> P = 0
+                        p1[r] = fast_exp2(fmaf(p1[r], sc2, -l1[r]));
+                        d0[r] = p0[r] * (d0[r] - r0[r]);
+                        d1[r] = p1[r] * (d1[r] - r1[r]);
+                    }
+                    pb = make_seqb<T>(p0, p1);
+                    dsb = make_seqb<T>(d0, d1);
+                }
 #pragma unroll
                 for (int t = 0; t < LY::NT; ++t) {
                     av[t] = mma_seq<T>(av[t], seqa_tr<T, DP>(Or, x0, t, lo), pb);

@@ -944,19 +944,20 @@ template <typename T, int DP> struct BwdLaunch {
                 a.nblk = 1;
                 const int nch = (a.L + CH - 1) / CH;
                 if constexpr (DP <= 64) {
-                    if (nch <= 3) {  // persistent, double-buffered with a loader wave (k_bwd_pipe)
-                        static_assert(BwdPipe<T, DP, 3>::FITS, "two buffers fit the LDS");
-                        const int thr = nch == 1   ? BwdPipe<T, DP, 1>::THREADS
-                                        : nch == 2 ? BwdPipe<T, DP, 2>::THREADS
-                                                   : BwdPipe<T, DP, 3>::THREADS;
-                        const void* kfn = nch == 1   ? reinterpret_cast<const void*>(k_bwd_pipe<T, DP, 1>)
-                                          : nch == 2 ? reinterpret_cast<const void*>(k_bwd_pipe<T, DP, 2>)
-                                                     : reinterpret_cast<const void*>(k_bwd_pipe<T, DP, 3>);
-                        const dim3 pg(persistent_grid(kfn, thr, bh)), blk(thr);
-                        if (nch == 1) hipLaunchKernelGGL((k_bwd_pipe<T, DP, 1>), pg, blk, 0, s, a);
-                        if (nch == 2) hipLaunchKernelGGL((k_bwd_pipe<T, DP, 2>), pg, blk, 0, s, a);
-                        if (nch == 3) hipLaunchKernelGGL((k_bwd_pipe<T, DP, 3>), pg, blk, 0, s, a);
+                    // persistent, double-buffered with a loader wave (k_bwd_pipe); four chunks recompute P and dS
+                    static_assert(BwdPipe<T, DP, 3>::FITS && BwdPipe<T, DP, 4>::FITS, "two buffers fit the LDS");
+                    auto pipe = [&](auto nchc) {
+                        constexpr int N = decltype(nchc)::value;
+                        const int thr = BwdPipe<T, DP, N>::THREADS;
+                        const dim3 pg(persistent_grid(reinterpret_cast<const void*>(k_bwd_pipe<T, DP, N>), thr, bh));
+                        hipLaunchKernelGGL((k_bwd_pipe<T, DP, N>), pg, dim3(thr), 0, s, a);
                         return launch_rc();
+                    };
+                    switch (nch) {
+                        case 1: return pipe(std::integral_constant<int, 1>{});
+                        case 2: return pipe(std::integral_constant<int, 2>{});
+                        case 3: return pipe(std::integral_constant<int, 3>{});
+                        default: return pipe(std::integral_constant<int, 4>{});
                     }
                 }
                 const dim3 grid((int)bh), block(fused_threads(a.L));
