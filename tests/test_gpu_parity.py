@@ -357,4 +357,7 @@ def test_bad_arguments_raise(cuda):
     with pytest.raises(ValueError):  # D > 128: the kernels' registers and LDS hold at most 128 per row
         x = torch.randn(1, 1, 4, 136, device=cuda)
         torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
+    with pytest.raises(ValueError):  # rows but no head dim
+        x = torch.randn(1, 1, 4, 0, device=cuda)
+        torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
     assert math.isfinite(1.0)
