@@ -303,7 +303,7 @@ def bwd_kernel_name(cfg: dict) -> str:
         return f"k_bwd_row<{DT_NAME[dt]}, {D}> + k_bwd_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32
-        kern = "k_bwd_pipe" if D <= 64 else "k_bwd_res"
+        kern = "k_bwd_pipe" if D <= 64 or nch <= 2 else "k_bwd_res"
         return f"{kern}<{DT_NAME[dt]}, {D}, {nch}>"
     return f"k_bwd_fused<{DT_NAME[dt]}>"
 

@@ -436,12 +436,14 @@ template <typename T, int DP, int NCH> struct BwdPipe {
     static constexpr int TB = LP * TP;            // one tile
     static constexpr int NWC = 2 * NCH;           // compute waves
     static constexpr int BUF = 4 * RB;            // K, V, Q, dO
-    // Up to three 32-row chunks the P and dS tiles fit beside the two buffers (5 GEMM units); with four (L up to 128)
-    // they do not, and the col pass recomputes P and dS from the buffer instead (7 GEMM units, loads still overlapped).
-    static constexpr bool TILES = NCH <= 3;
+    // Where the P and dS tiles fit beside the two buffers (D = 64: up to three 32-row chunks; D = 128: one) the col
+    // pass reads them (5 GEMM units); otherwise it recomputes P and dS from the buffer (7 GEMM units, loads still
+    // overlapped with the previous slice's work).
+    static constexpr int STORES = NWC * RowStage16<T, DP>::BYTES;
+    static constexpr bool TILES = 2 * BUF + 2 * TB + 4 * LP * 4 + STORES <= 160 * 1024;
     static constexpr int STG = 2 * BUF + (TILES ? 2 * TB : 0) + 4 * LP * 4;  // byte offset of the store areas
     // two buffers | P, dS tiles | lse * log2 e (two) | rowsum(dO o O) (two) | a row-store area per compute wave
-    static constexpr int SMEM = STG + NWC * RowStage16<T, DP>::BYTES;
+    static constexpr int SMEM = STG + STORES;
     static constexpr int THREADS = 64 * (NWC + 1);
     static constexpr bool FITS = SMEM <= 160 * 1024;
 };
@@ -499,9 +501,10 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NC
     if (w.wave == R::NWC) {
         // ---- loader wave: lane t handles rows t and t + 64 for lse and rowsum(dO o O)
         constexpr int NCK = Sw<DP>::NCK;
+        constexpr bool TWO = Lp > 64;  // a second row per lane
         const int t0 = w.lane, t1 = w.lane + 64;
         float lv0 = 0.f, lv1 = 0.f;
-        u32x4 o0[NCK], o1[NCK];  // O rows t0, t1 (rows past L: row L - 1, finite; their rowsum is written as 0)
+        u32x4 o0[NCK], o1[TWO ? NCK : 1];  // O rows t0, t1 (rows past L: row L - 1, finite; rowsum written as 0)
         auto issue = [&](int sl, int bsel) {
             const int b = sl / a.H, h = sl - b * a.H;
             unsigned char* base = smem + bsel * R::BUF;
@@ -510,14 +513,15 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NC
             async_rows<T, DP>(base + 2 * R::RB, slice<T>(a.q, b, h), a.q.sl, L, Lp, 0, 1, w.lane);
             async_rows<T, DP>(base + 3 * R::RB, slice<T>(a.dO, b, h), a.dO.sl, L, Lp, 0, 1, w.lane);
             lv0 = a.lse[(int64_t)sl * L + (t0 < L ? t0 : L - 1)];  // unconditional loads
-            lv1 = a.lse[(int64_t)sl * L + (t1 < L ? t1 : L - 1)];
             const T* ob = reinterpret_cast<const T*>(a.o) + (int64_t)sl * L * DP;
             const T* p0 = ob + (int64_t)(t0 < L ? t0 : L - 1) * DP;
-            const T* p1 = ob + (int64_t)(t1 < L ? t1 : L - 1) * DP;
 #pragma unroll
-            for (int c = 0; c < NCK; ++c) {
-                o0[c] = *reinterpret_cast<const u32x4*>(p0 + 8 * c);
-                o1[c] = *reinterpret_cast<const u32x4*>(p1 + 8 * c);
+            for (int c = 0; c < NCK; ++c) o0[c] = *reinterpret_cast<const u32x4*>(p0 + 8 * c);
+            if constexpr (TWO) {
+                lv1 = a.lse[(int64_t)sl * L + (t1 < L ? t1 : L - 1)];
+                const T* p1 = ob + (int64_t)(t1 < L ? t1 : L - 1) * DP;
+#pragma unroll
+                for (int c = 0; c < NCK; ++c) o1[c] = *reinterpret_cast<const u32x4*>(p1 + 8 * c);
             }
         };
         auto rowsum = [&](const unsigned char* dor, int t, const u32x4(&o)[NCK]) {
@@ -535,9 +539,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NC
                 l2[t0] = t0 < L ? lv0 * LOG2E : INFINITY;  // padded query rows: P = 0
                 d2[t0] = rowsum(dor, t0, o0);
             }
-            if (t1 < Lp) {
-                l2[t1] = t1 < L ? lv1 * LOG2E : INFINITY;
-                d2[t1] = rowsum(dor, t1, o1);
+            if constexpr (TWO) {
+                if (t1 < Lp) {
+                    l2[t1] = t1 < L ? lv1 * LOG2E : INFINITY;
+                    d2[t1] = rowsum(dor, t1, o1);
+                }
             }
         };
         issue(s, 0);

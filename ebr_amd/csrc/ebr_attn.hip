@@ -943,22 +943,26 @@ template <typename T, int DP> struct BwdLaunch {
             if (resident_shape(a, DP, 2, true)) {
                 a.nblk = 1;
                 const int nch = (a.L + CH - 1) / CH;
+                // persistent, double-buffered with a loader wave (k_bwd_pipe), wherever two buffers of K, V, Q, dO
+                // fit the LDS: D <= 64 up to four chunks, D = 128 up to two (the P and dS tiles where they fit too)
+                auto pipe = [&](auto nchc) {
+                    constexpr int N = decltype(nchc)::value;
+                    static_assert(BwdPipe<T, DP, N>::FITS, "two buffers fit the LDS");
+                    const int thr = BwdPipe<T, DP, N>::THREADS;
+                    const dim3 pg(persistent_grid(reinterpret_cast<const void*>(k_bwd_pipe<T, DP, N>), thr, bh));
+                    hipLaunchKernelGGL((k_bwd_pipe<T, DP, N>), pg, dim3(thr), 0, s, a);
+                    return launch_rc();
+                };
                 if constexpr (DP <= 64) {
-                    // persistent, double-buffered with a loader wave (k_bwd_pipe); four chunks recompute P and dS
-                    static_assert(BwdPipe<T, DP, 3>::FITS && BwdPipe<T, DP, 4>::FITS, "two buffers fit the LDS");
-                    auto pipe = [&](auto nchc) {
-                        constexpr int N = decltype(nchc)::value;
-                        const int thr = BwdPipe<T, DP, N>::THREADS;
-                        const dim3 pg(persistent_grid(reinterpret_cast<const void*>(k_bwd_pipe<T, DP, N>), thr, bh));
-                        hipLaunchKernelGGL((k_bwd_pipe<T, DP, N>), pg, dim3(thr), 0, s, a);
-                        return launch_rc();
-                    };
                     switch (nch) {
                         case 1: return pipe(std::integral_constant<int, 1>{});
                         case 2: return pipe(std::integral_constant<int, 2>{});
                         case 3: return pipe(std::integral_constant<int, 3>{});
                         default: return pipe(std::integral_constant<int, 4>{});
                     }
+                } else {
+                    if (nch == 1) return pipe(std::integral_constant<int, 1>{});
+                    if (nch == 2) return pipe(std::integral_constant<int, 2>{});
                 }
                 const dim3 grid((int)bh), block(fused_threads(a.L));
                 switch (nch) {
