@@ -288,7 +288,7 @@ def bb_kernel_name(cfg: dict) -> str:
         return f"k_bb_row<{DT_NAME[dt]}, {D}> + k_bb_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32
-        kern = "k_bb_share" if D <= 64 and nch <= 3 else "k_bb_res"  # contiguous inputs: row strides fit
+        kern = "k_bb_share" if (D <= 64 and nch <= 3) or nch <= 2 else "k_bb_res"  # contiguous: row strides fit
         return f"{kern}<{DT_NAME[dt]}, {D}, {nch}>"
     return f"k_bb_fused<{DT_NAME[dt]}>"
 

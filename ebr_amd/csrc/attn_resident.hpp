@@ -920,8 +920,11 @@ template <typename T, int DP, int NCH> struct BbShare {
     static constexpr int TP = LP * 2 + 32;        // tile row pitch (bytes), padded off the 256-byte bank period
     static constexpr int TB = LP * TP;            // one tile
     static constexpr int NWC = 2 * NCH;           // compute waves (16 rows each)
-    static constexpr int NWL = 2;                 // loader waves
     static constexpr int NB = LP / Sw<DP>::RPI;   // 1 KB blocks per tensor
+    // loader waves: each holds NB / NWL of the 1 KB blocks of each of the 8 staged tensors in registers (32 NB / NWL
+    // VGPRs); two, or four where two would need more than 192 VGPRs each (only D = 128 with two chunks)
+    static constexpr int NWL = 32 * NB / 2 > 192 ? 4 : 2;
+    static_assert(NWC + NWL <= 8, "launch bound of 512 threads");
     static constexpr int NPER = NB / NWL;         // blocks per loader wave and tensor
     static_assert(NPER * NWL == NB, "the loader waves split every tensor's 1 KB blocks evenly");
     static_assert(NWL * 64 >= LP, "one loader lane per row for lse");

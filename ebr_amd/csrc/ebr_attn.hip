@@ -1018,19 +1018,21 @@ template <typename T, int DP> struct BbLaunch {
                 hipLaunchKernelGGL((k_bb_fused<T, DP>), grid, block, 0, s, a);
             } else if constexpr (!ET<T>::F32) {
                 const int nch = (a.L + CH - 1) / CH;
-                if constexpr (DP <= 64) {
-                    if (nch <= 3 && struct_strides_fit(a)) {  // tiles shared through LDS (k_bb_share)
-                        const int thr = nch == 1 ? BbShare<T, DP, 1>::THREADS
-                                        : nch == 2 ? BbShare<T, DP, 2>::THREADS
-                                                   : BbShare<T, DP, 3>::THREADS;
-                        const void* kfn = nch == 1   ? reinterpret_cast<const void*>(k_bb_share<T, DP, 1>)
-                                          : nch == 2 ? reinterpret_cast<const void*>(k_bb_share<T, DP, 2>)
-                                                     : reinterpret_cast<const void*>(k_bb_share<T, DP, 3>);
-                        const dim3 pg(persistent_grid(kfn, thr, bh)), blk(thr);
-                        if (nch == 1) hipLaunchKernelGGL((k_bb_share<T, DP, 1>), pg, blk, 0, s, a);
-                        if (nch == 2) hipLaunchKernelGGL((k_bb_share<T, DP, 2>), pg, blk, 0, s, a);
-                        if (nch == 3) hipLaunchKernelGGL((k_bb_share<T, DP, 3>), pg, blk, 0, s, a);
-                        return launch_rc();
+                // tiles shared through LDS, persistent with loader waves (k_bb_share), where its regions fit the LDS:
+                // D <= 64 up to three chunks, D = 128 up to two
+                auto share = [&](auto nchc) {
+                    constexpr int N = decltype(nchc)::value;
+                    static_assert(BbShare<T, DP, N>::SMEM <= 160 * 1024, "the regions fit the LDS");
+                    const int thr = BbShare<T, DP, N>::THREADS;
+                    const dim3 pg(persistent_grid(reinterpret_cast<const void*>(k_bb_share<T, DP, N>), thr, bh));
+                    hipLaunchKernelGGL((k_bb_share<T, DP, N>), pg, dim3(thr), 0, s, a);
+                    return launch_rc();
+                };
+                if (struct_strides_fit(a)) {
+                    if (nch == 1) return share(std::integral_constant<int, 1>{});
+                    if (nch == 2) return share(std::integral_constant<int, 2>{});
+                    if constexpr (DP <= 64) {
+                        if (nch == 3) return share(std::integral_constant<int, 3>{});
                     }
                 }
                 switch (nch) {
