@@ -259,6 +259,12 @@ def cpu_baseline(cfg, scale, nbh: int = 0, reps: int = 5):
     }
 
 
+def phase_speedups(leg: dict, cb: dict) -> dict:
+    """GPU over CPU throughput per phase (TFLOP/s ratios, so a CPU sample of fewer slices compares fairly)."""
+    return {p: round(v["tflops"] / cb["phase_tflops"][p], 1) for p, v in leg["phases"].items()
+            if cb.get("phase_tflops", {}).get(p)}
+
+
 def cpu_info() -> dict:
     """The host CPU's model name, its logical CPU count, and which of the ISA extensions that matter to the eager
     baseline's bf16 / fp32 GEMMs it reports."""
@@ -902,6 +908,7 @@ def main() -> int:
     ap.add_argument("--no-ebr-infer", action="store_true", help="skip the inference descent (config 4)")
     ap.add_argument("--ebr-steps", type=int, default=10)
     ap.add_argument("--no-maze", action="store_true", help="skip the Maze (config 2) attention leg")
+    ap.add_argument("--no-config0", action="store_true", help="skip the N-Queens 8x8 fp32 (config 0) attention leg")
     ap.add_argument("--no-config4-attn", action="store_true", help="skip config 4's attention shape (fwd + bwd)")
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
     ap.add_argument("--descent-target", action="store_true", help="run only the descent-wrapper leg (for rocprofv3)")
@@ -983,15 +990,23 @@ def main() -> int:
         cb = cpu_baseline(cfg, scale)
         out["cpu_baseline"] = cb
         out["speedup_vs_cpu"] = round(head["tflops"] / cb["value"], 1) if cb["value"] > 0 else None
+        out["speedup_vs_cpu_phases"] = phase_speedups(head, cb)
         err = spot_check(sample, scale)
         log(f"spot-check max rel err vs CPU oracle on 16 slices: {err:.3e}")
         out["parity_max_rel_err"] = float(f"{err:.3e}")
     else:
         out["cpu_baseline"] = None
+    if not args.no_config0 and args.config != 0:
+        out["config0"] = attn_leg(CONFIGS[0], max(10, args.steps // 5), 3, PHASES, args.kernel_reps)
+        if not args.no_cpu:
+            out["config0"]["cpu_baseline"] = cpu_baseline(CONFIGS[0], 64**-0.5)
+            out["config0"]["speedup_vs_cpu_phases"] = phase_speedups(out["config0"], out["config0"]["cpu_baseline"])
+        log(f"config0: {out['config0']}")
     if not args.no_maze and args.config != 2:
         out["maze"] = attn_leg(CONFIGS[2], max(10, args.steps // 5), 3, PHASES, args.kernel_reps)
         if not args.no_cpu:
             out["maze"]["cpu_baseline"] = cpu_baseline(CONFIGS[2], 64**-0.5, nbh=32)
+            out["maze"]["speedup_vs_cpu_phases"] = phase_speedups(out["maze"], out["maze"]["cpu_baseline"])
         log(f"maze: {out['maze']}")
         torch.cuda.empty_cache()
     if not args.no_config4_attn:
