@@ -683,6 +683,235 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NC
 }
 
 // =====================================================================================================================
+// Backward, persistent with a loader wave for shapes whose two full buffers do not fit the LDS (D = 128, 65 <= L <= 112):
+// one K, V region (X) and one Q, dO region (Y), each filled one pass ahead of its use.
+//   compute waves                                  loader wave
+//   row pass (s): dQ from X; own K, V rows -> regs  loads Y <- Q, dO of slice s
+//   --- barrier A: X free, Y holds s
+//   col pass (s): dK, dV from Y (P, dS recomputed);  loads X <- K, V of slice n = s + G
+//                 own Q, dO, O rows of n -> regs
+//   --- barrier B: Y free, X holds n
+// The row pass takes its own Q, dO rows (and O, for Dr = rowsum(dO o O)) from global memory, loaded during the
+// previous col pass: that is the one input read twice (the second read, Y's, a few microseconds later). 7 GEMM units
+// as in k_bwd_res, with the loads of the next slice overlapped with this one's work.
+// =====================================================================================================================
+
+constexpr int bwd_pp_waves(int nch) { return 2 * nch > 7 ? 7 : 2 * nch; }  // compute waves (16 rows each)
+
+template <typename T, int DP, int NCH> struct BwdPP {
+    static constexpr int LP = NCH * CH;
+    static constexpr int RB = LP * Sw<DP>::ROWB;
+    static constexpr int NWC = bwd_pp_waves(NCH);           // L <= 16 NWC
+    static constexpr int ST = 4 * RB;                       // lse * log2 e [LP] | Dr [LP]
+    static constexpr int STG = ST + 2 * LP * 4;             // a row-store area per compute wave
+    static constexpr int SMEM = STG + NWC * RowStage16<T, DP>::BYTES;
+    static constexpr int THREADS = 64 * (NWC + 1);
+    static constexpr bool FITS = SMEM <= 160 * 1024;
+};
+
+template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp_waves(NCH) + 1)) void k_bwd_pp(Args a) {
+    using LY = Lay<T, DP>;
+    using R = BwdPP<T, DP, NCH>;
+    constexpr int Lp = R::LP;
+    __shared__ __align__(1024) unsigned char smem[R::SMEM];
+    unsigned char* Kr = smem;
+    unsigned char* Vr = smem + R::RB;
+    unsigned char* Qr = smem + 2 * R::RB;
+    unsigned char* Or = smem + 3 * R::RB;  // dO
+    float* l2s = reinterpret_cast<float*>(smem + R::ST);
+    float* drs = l2s + Lp;
+    const WaveIds w = wave_ids();
+    const int L = a.L;
+    const int nbh = a.B * a.H;
+    int s = blockIdx.x;
+    if (s >= nbh) return;  // uniform over the workgroup
+
+    if (w.wave == R::NWC) {
+        // ---- loader wave; statistics rows of no active wave (past L rounded up to 16): P = 0 and Dr = 0 there
+        for (int x = (L + 15) / 16 * 16 + w.lane; x < Lp; x += 64) {
+            l2s[x] = INFINITY;
+            drs[x] = 0.f;
+        }
+        auto region2 = [&](unsigned char* r0, const Strided& t0, unsigned char* r1, const Strided& t1, int sl) {
+            const int b = sl / a.H, h = sl - b * a.H;
+            async_rows<T, DP>(r0, slice<T>(t0, b, h), t0.sl, L, Lp, 0, 1, w.lane);
+            async_rows<T, DP>(r1, slice<T>(t1, b, h), t1.sl, L, Lp, 0, 1, w.lane);
+        };
+        region2(Kr, a.k, Vr, a.v, s);
+        async_wait();
+        lds_barrier();  // X holds the first slice
+        for (;;) {
+            region2(Qr, a.q, Or, a.dO, s);
+            async_wait();
+            lds_barrier();  // A
+            const int n = s + (int)gridDim.x;
+            const bool more = n < nbh;
+            if (more) region2(Kr, a.k, Vr, a.v, n);
+            async_wait();
+            lds_barrier();  // B
+            if (!more) break;
+            s = n;
+        }
+        return;
+    }
+
+    // ---- compute waves
+    const float sc = a.scale;
+    const float sc2 = sc * LOG2E;
+    const int row0 = w.wave * 16;
+    const int own = row0 + w.l16;
+    const bool active = row0 < L;  // wave-uniform; inactive waves still take every barrier
+    const LaneOff<T, DP> lo(w.l16, w.g);
+    unsigned char* stage = smem + R::STG + w.wave * RowStage16<T, DP>::BYTES;
+    // Own rows of the slice the next row pass works on, loaded from global memory a pass or two ahead: dO, O (for Dr)
+    // and lse during the row pass before, Q during the col pass before. The loads read row min(own, L - 1) and are
+    // not masked until their first use, so that nothing waits for them before then (rows past L are zeroed there).
+    OwnFrag<T, DP> qf, df;
+    float lraw = 0.f, dr = 0.f;
+    const int orow = own < L ? own : L - 1;
+    auto own_raw = [&](const T* base, int64_t srow, OwnFrag<T, DP>& f) {
+        const T* p = base + (int64_t)orow * srow + w.g * LY::VEC;
+#pragma unroll
+        for (int c = 0; c < LY::NC; ++c) f.v[c] = *reinterpret_cast<const u32x4*>(p + c * LY::CW);
+    };
+    auto own_rows = [&](const Strided& t, int sl, OwnFrag<T, DP>& f) {
+        const int b = sl / a.H, h = sl - b * a.H;
+        own_raw(slice<T>(t, b, h), t.sl, f);
+    };
+    auto own_o = [&](int sl, OwnFrag<T, DP>& f) {
+        own_raw(reinterpret_cast<const T*>(a.o) + (int64_t)sl * L * DP, DP, f);
+    };
+    auto own_lse = [&](int sl) { return a.lse[(int64_t)sl * L + orow]; };
+    auto zero_past_l = [&](OwnFrag<T, DP>& f) {
+#pragma unroll
+        for (int c = 0; c < LY::NC; ++c) f.v[c] = own < L ? f.v[c] : u32x4{0u, 0u, 0u, 0u};
+    };
+    if (active) {
+        OwnFrag<T, DP> of;
+        own_rows(a.q, s, qf);
+        own_rows(a.dO, s, df);
+        own_o(s, of);
+        lraw = own_lse(s);
+        dr = own < L ? xsum4(frag_dot<T, DP>(df, of)) : 0.f;
+    }
+    lds_barrier();  // X holds the first slice
+    for (;;) {
+        const int n = s + (int)gridDim.x;
+        const bool more = n < nbh;
+        OwnFrag<T, DP> kf, vf, qn, dn;
+        float lrn = 0.f, drn = 0.f;
+
+        // ---- row pass: own = queries; dQ
+        if (active) {
+            OwnFrag<T, DP> on;
+            if (more) {
+                own_rows(a.dO, n, dn);
+                own_o(n, on);
+                lrn = own_lse(n);
+            }
+            zero_past_l(qf);
+            zero_past_l(df);
+            const float lse2 = (own < L) ? lraw * LOG2E : 0.f;
+            if (w.g == 0) {
+                l2s[own] = (own < L) ? lse2 : INFINITY;  // padded query rows: P = 0
+                drs[own] = (own < L) ? dr : 0.f;
+            }
+            f32x4 acc[LY::NT];
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                constexpr bool LAST = C == NCH - 1;
+                const int x0 = C * CH;
+                f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+                mma_d_sw<T, DP>(p0, Kr, x0, qf, lo);
+                mma_d_sw<T, DP>(p1, Kr, x0 + 16, qf, lo);
+                mma_d_sw<T, DP>(d0, Vr, x0, df, lo);
+                mma_d_sw<T, DP>(d1, Vr, x0 + 16, df, lo);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int x = x0 + 4 * w.g + r;
+                    p0[r] = row_p<LAST>(p0[r], sc2, lse2, x, L);
+                    p1[r] = row_p<LAST>(p1[r], sc2, lse2, x + 16, L);
+                    d0[r] = p0[r] * (d0[r] - dr);
+                    d1[r] = p1[r] * (d1[r] - dr);
+                }
+                const SeqB<T> dsb = make_seqb<T>(d0, d1);
+#pragma unroll
+                for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, x0, t, lo), dsb);
+            });
+            own_from_lds<T, DP>(kf, Kr, row0, lo);
+            own_from_lds<T, DP>(vf, Vr, row0, lo);
+            store_acc_staged<T, DP>(a.out0, ((int64_t)s * L + row0) * DP, L - row0, acc, sc, stage, w.lane);
+            if (more) drn = own < L ? xsum4(frag_dot<T, DP>(dn, on)) : 0.f;
+        }
+        lds_barrier();  // A: statistics published, X free, Y holds slice s
+
+        // ---- col pass: own = keys; dK = s dS^T Q, dV = P^T dO with P and dS recomputed. P and dS of every chunk are
+        // kept as packed MFMA operands and the products run one half of the d tiles at a time, so that only half
+        // of dK and dV is accumulated in fp32 at once.
+        if (active) {
+            if (more) own_rows(a.q, n, qn);  // lands during the col pass
+            SeqB<T> pbs[NCH], dsbs[NCH];
+            static_for<0, NCH>([&](auto cc) {
+                constexpr int C = decltype(cc)::value;
+                const int x0 = C * CH;
+                const f32x4 l0 = *reinterpret_cast<const f32x4*>(l2s + x0 + 4 * w.g);
+                const f32x4 l1 = *reinterpret_cast<const f32x4*>(l2s + x0 + 16 + 4 * w.g);
+                const f32x4 r0 = *reinterpret_cast<const f32x4*>(drs + x0 + 4 * w.g);
+                const f32x4 r1 = *reinterpret_cast<const f32x4*>(drs + x0 + 16 + 4 * w.g);
+                f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+                mma_d_sw<T, DP>(p0, Qr, x0, kf, lo);
+                mma_d_sw<T, DP>(p1, Qr, x0 + 16, kf, lo);
+                mma_d_sw<T, DP>(d0, Or, x0, vf, lo);
+                mma_d_sw<T, DP>(d1, Or, x0 + 16, vf, lo);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    p0[r] = fast_exp2(fmaf(p0[r], sc2, -l0[r]));  // lse = +inf on padded query rows -> P = 0
+                    p1[r] = fast_exp2(fmaf(p1[r], sc2, -l1[r]));
+                    d0[r] = p0[r] * (d0[r] - r0[r]);
+                    d1[r] = p1[r] * (d1[r] - r1[r]);
+                }
+                pbs[C] = make_seqb<T>(p0, p1);
+                dsbs[C] = make_seqb<T>(d0, d1);
+            });
+            constexpr int NH = LY::NT / 2;
+            u32x2 pk_k[LY::NT], pk_v[LY::NT];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                f32x4 ak[NH], av[NH];
+#pragma unroll
+                for (int t = 0; t < NH; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                static_for<0, NCH>([&](auto cc) {
+                    constexpr int C = decltype(cc)::value;
+                    const int x0 = C * CH;
+#pragma unroll
+                    for (int t = 0; t < NH; ++t) {
+                        av[t] = mma_seq<T>(av[t], seqa_tr<T, DP>(Or, x0, half * NH + t, lo), pbs[C]);
+                        ak[t] = mma_seq<T>(ak[t], seqa_tr<T, DP>(Qr, x0, half * NH + t, lo), dsbs[C]);
+                    }
+                });
+#pragma unroll
+                for (int t = 0; t < NH; ++t) {
+                    pk_k[half * NH + t] = pack4<T>(ak[t] * sc);
+                    pk_v[half * NH + t] = pack4<T>(av[t]);
+                }
+            }
+            const int64_t r = ((int64_t)s * L + row0) * DP;
+            store_rows_staged<T, DP>(a.out1, r, L - row0, pk_k, stage, w.lane);
+            store_rows_staged<T, DP>(a.out2, r, L - row0, pk_v, stage, w.lane);
+        }
+        lds_barrier();  // B: Y free, X holds slice n
+        if (!more) break;
+        s = n;
+        qf = qn;
+        df = dn;
+        lraw = lrn;
+        dr = drn;
+    }
+}
+
+// =====================================================================================================================
 // Backward of the backward: register-resident row pass, then the col pass.
 // Row pass, phase 1: the wave's 16 query rows x all keys of P, dS, M1 = dS A + P Bm and PA = P A, kept as packed
 // 16-bit MFMA operands, and the exact E = rowsum(PA), T = rowsum(M1). Phase 2: dS2 = M1 - E dS - T P and

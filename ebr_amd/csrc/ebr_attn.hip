@@ -944,7 +944,8 @@ template <typename T, int DP> struct BwdLaunch {
                 a.nblk = 1;
                 const int nch = (a.L + CH - 1) / CH;
                 // persistent, double-buffered with a loader wave (k_bwd_pipe), wherever two buffers of K, V, Q, dO
-                // fit the LDS: D <= 64 up to four chunks, D = 128 up to two (the P and dS tiles where they fit too)
+                // fit the LDS: D <= 64 up to four chunks, D = 128 up to two (the P and dS tiles where they fit too);
+                // D = 128 with three chunks, or four up to L = 112, runs k_bwd_pp
                 auto pipe = [&](auto nchc) {
                     constexpr int N = decltype(nchc)::value;
                     static_assert(BwdPipe<T, DP, N>::FITS, "two buffers fit the LDS");
@@ -963,6 +964,17 @@ template <typename T, int DP> struct BwdLaunch {
                 } else {
                     if (nch == 1) return pipe(std::integral_constant<int, 1>{});
                     if (nch == 2) return pipe(std::integral_constant<int, 2>{});
+                    // one K, V and one Q, dO region, each loaded a pass ahead (k_bwd_pp), up to 7 compute waves
+                    auto pp = [&](auto nchc) {
+                        constexpr int N = decltype(nchc)::value;
+                        static_assert(BwdPP<T, DP, N>::FITS, "the two regions and the store areas fit the LDS");
+                        const int thr = BwdPP<T, DP, N>::THREADS;
+                        const dim3 pg(persistent_grid(reinterpret_cast<const void*>(k_bwd_pp<T, DP, N>), thr, bh));
+                        hipLaunchKernelGGL((k_bwd_pp<T, DP, N>), pg, dim3(thr), 0, s, a);
+                        return launch_rc();
+                    };
+                    if (nch == 3) return pp(std::integral_constant<int, 3>{});
+                    if (a.L <= 16 * BwdPP<T, DP, 4>::NWC) return pp(std::integral_constant<int, 4>{});
                 }
                 const dim3 grid((int)bh), block(fused_threads(a.L));
                 switch (nch) {

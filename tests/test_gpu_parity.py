@@ -232,12 +232,14 @@ def test_wide_row_stride(cuda):
 
 # (B, H, L, D): more slices than the persistent kernels' grid (one workgroup per CU times the workgroups a CU holds),
 # with a remainder, for one to four 32-key chunks and every head dim the persistent kernels take: at D = 128 the
-# backward (one and two chunks) and the backward of the backward (with four loader waves at two chunks); at D = 32 and
-# 64 with four chunks the backward (tiles at D = 32, recomputed P and dS at D = 64).
+# backward (one and two chunks; three, and four up to L = 112, with one region of each kind; L = 113 past that) and
+# the backward of the backward (with four loader waves at two chunks); at D = 32 and 64 with four chunks the backward
+# (tiles at D = 32, recomputed P and dS at D = 64).
 @pytest.mark.parametrize(
     "B,H,L,D",
     [(75, 4, 81, 64), (130, 8, 20, 64), (70, 8, 50, 32), (90, 6, 96, 32), (101, 6, 100, 32), (99, 6, 113, 64),
-     (140, 4, 28, 128), (130, 4, 45, 128), (129, 4, 64, 128)],
+     (140, 4, 28, 128), (130, 4, 45, 128), (129, 4, 64, 128), (70, 4, 70, 128), (67, 4, 100, 128),
+     (65, 4, 112, 128), (66, 4, 113, 128)],
 )
 def test_persistent_many_slices(cuda, B, H, L, D):
     _case(B, H, L, D, torch.bfloat16, cuda, seed=L + D)
