@@ -763,11 +763,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
     const bool active = row0 < L;  // wave-uniform; inactive waves still take every barrier
     const LaneOff<T, DP> lo(w.l16, w.g);
     unsigned char* stage = smem + R::STG + w.wave * RowStage16<T, DP>::BYTES;
-    // Own rows of the slice the next row pass works on, loaded from global memory a pass or two ahead: dO, O (for Dr)
-    // and lse during the row pass before, Q during the col pass before. The loads read row min(own, L - 1) and are
-    // not masked until their first use, so that nothing waits for them before then (rows past L are zeroed there).
-    OwnFrag<T, DP> qf, df;
-    float lraw = 0.f, dr = 0.f;
+    // Own Q, dO, O rows and lse of the slice the next row pass works on, loaded from global memory at the start of
+    // the col pass before it and first used after the barrier that ends that pass, so that nothing waits for them
+    // in between. The loads read row min(own, L - 1); rows past L are zeroed at their use.
+    OwnFrag<T, DP> qf, df, of;
+    float lraw = 0.f;
     const int orow = own < L ? own : L - 1;
     auto own_raw = [&](const T* base, int64_t srow, OwnFrag<T, DP>& f) {
         const T* p = base + (int64_t)orow * srow + w.g * LY::VEC;
@@ -787,28 +787,21 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
         for (int c = 0; c < LY::NC; ++c) f.v[c] = own < L ? f.v[c] : u32x4{0u, 0u, 0u, 0u};
     };
     if (active) {
-        OwnFrag<T, DP> of;
         own_rows(a.q, s, qf);
         own_rows(a.dO, s, df);
         own_o(s, of);
         lraw = own_lse(s);
-        dr = own < L ? xsum4(frag_dot<T, DP>(df, of)) : 0.f;
     }
     lds_barrier();  // X holds the first slice
     for (;;) {
         const int n = s + (int)gridDim.x;
         const bool more = n < nbh;
-        OwnFrag<T, DP> kf, vf, qn, dn;
-        float lrn = 0.f, drn = 0.f;
+        OwnFrag<T, DP> kf, vf, qn, dn, on;
+        float lrn;  // set with qn, dn, on where ``more``; read only then
 
         // ---- row pass: own = queries; dQ
         if (active) {
-            OwnFrag<T, DP> on;
-            if (more) {
-                own_rows(a.dO, n, dn);
-                own_o(n, on);
-                lrn = own_lse(n);
-            }
+            const float dr = own < L ? xsum4(frag_dot<T, DP>(df, of)) : 0.f;
             zero_past_l(qf);
             zero_past_l(df);
             const float lse2 = (own < L) ? lraw * LOG2E : 0.f;
@@ -843,7 +836,6 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
             own_from_lds<T, DP>(kf, Kr, row0, lo);
             own_from_lds<T, DP>(vf, Vr, row0, lo);
             store_acc_staged<T, DP>(a.out0, ((int64_t)s * L + row0) * DP, L - row0, acc, sc, stage, w.lane);
-            if (more) drn = own < L ? xsum4(frag_dot<T, DP>(dn, on)) : 0.f;
         }
         lds_barrier();  // A: statistics published, X free, Y holds slice s
 
@@ -851,7 +843,12 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
         // kept as packed MFMA operands and the products run one half of the d tiles at a time, so that only half
         // of dK and dV is accumulated in fp32 at once.
         if (active) {
-            if (more) own_rows(a.q, n, qn);  // lands during the col pass
+            if (more) {  // the next slice's own rows, landing during this pass
+                own_rows(a.q, n, qn);
+                own_rows(a.dO, n, dn);
+                own_o(n, on);
+                lrn = own_lse(n);
+            }
             SeqB<T> pbs[NCH], dsbs[NCH];
             static_for<0, NCH>([&](auto cc) {
                 constexpr int C = decltype(cc)::value;
@@ -906,8 +903,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
         s = n;
         qf = qn;
         df = dn;
+        of = on;
         lraw = lrn;
-        dr = drn;
     }
 }
 
