@@ -452,6 +452,32 @@ def multi_solution_bench(steps: int, warmup: int) -> dict:
     return out
 
 
+MULTI_TARGET_SETTLE, MULTI_TARGET_REPS = 1000, 20
+
+
+def multi_target(reps: int = MULTI_TARGET_REPS) -> None:
+    """The multi-solution shapes alone, for ``rocprofv3`` (kernel trace and --pmc passes): the same 256 MiB calibration
+    copy as ``pmc_target``, then per shape ``MULTI_TARGET_SETTLE`` untimed and ``reps`` timed fwd -> bwd -> bwd_bwd
+    steps on rotating input sets (fixed counts, so every profiling run dispatches the same sequence)."""
+    dev = torch.device("cuda", 0)
+    src = torch.empty(64 << 20, device=dev, dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    for B, H, L, D in MULTI_SOLUTION_SHAPES:
+        cfg = dict(name=f"B={B} H={H} L={L} D={D}", B=B, H=H, L=L, D=D, dtype=torch.bfloat16, qkv_scale=0.125)
+        sets = make_sets(cfg, dev, 3)
+        for i in range(MULTI_TARGET_SETTLE + reps):
+            step(sets[i % len(sets)], D**-0.5)
+        torch.cuda.synchronize()
+        for p in PHASES:
+            log(f"multi target L={L}: {p} algorithmic bytes per launch {roofline.phase_bytes(p, B, H, L, D, 2):.0f}")
+        del sets
+        torch.cuda.empty_cache()
+
+
 def descent_target(reps: int = 20) -> None:
     """The descent-wrapper leg alone, for ``rocprofv3`` (kernel trace and --pmc passes): the same 256 MiB calibration
     copy as ``pmc_target``, then ``descent_bench``'s timed launches; prints its JSON."""
@@ -913,6 +939,7 @@ def main() -> int:
     ap.add_argument("--pmc-target", action="store_true", help="run the short kernel sequence for rocprofv3 --pmc")
     ap.add_argument("--descent-target", action="store_true", help="run only the descent-wrapper leg (for rocprofv3)")
     ap.add_argument("--block-target", action="store_true", help="run only the energy-block leg (for rocprofv3)")
+    ap.add_argument("--multi-target", action="store_true", help="run only the multi-solution shapes (for rocprofv3)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
@@ -942,6 +969,9 @@ def main() -> int:
         return 0
     if args.block_target:
         block_target()
+        return 0
+    if args.multi_target:
+        multi_target()
         return 0
     cfg = CONFIGS[args.config]
     if args.pmc_target:
