@@ -266,20 +266,26 @@ def phase_speedups(leg: dict, cb: dict) -> dict:
 
 
 def cpu_info() -> dict:
-    """The host CPU's model name, its logical CPU count, and which of the ISA extensions that matter to the eager
-    baseline's bf16 / fp32 GEMMs it reports."""
-    model, flags = "unknown", set()
+    """The host CPU's model name with its family / model / stepping numbers (a virtualised host may report only a
+    generic name), its logical CPU count, and which of the ISA extensions that matter to the eager baseline's bf16 /
+    fp32 GEMMs it reports."""
+    model, flags, ids = "unknown", set(), {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name") and model == "unknown":
-                    model = line.split(":", 1)[1].strip()
-                elif line.startswith("flags") and not flags:
-                    flags = set(line.split(":", 1)[1].split())
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key == "model name" and model == "unknown":
+                    model = val.strip()
+                elif key in ("cpu family", "model", "stepping") and key not in ids:
+                    ids[key] = val.strip()
+                elif key == "flags" and not flags:
+                    flags = set(val.split())
     except OSError:
         pass
     isa = ["avx2", "fma", "avx512f", "avx512_bf16", "avx512_vnni", "avx512_fp16", "amx_tile", "amx_bf16"]
-    return {"model": model, "logical_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+    return {"model": model, "family_model_stepping": "/".join(ids.get(k, "?") for k in ("cpu family", "model", "stepping")),
+            "logical_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
             "isa": {f: f in flags for f in isa}}
 
 
@@ -309,7 +315,7 @@ def bwd_kernel_name(cfg: dict) -> str:
         return f"k_bwd_row<{DT_NAME[dt]}, {D}> + k_bwd_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32
-        kern = "k_bwd_pipe" if D <= 64 or nch <= 2 else "k_bwd_res"
+        kern = "k_bwd_pipe" if D <= 64 or nch <= 2 else ("k_bwd_pp" if L <= 112 else "k_bwd_res")
         return f"{kern}<{DT_NAME[dt]}, {D}, {nch}>"
     return f"k_bwd_fused<{DT_NAME[dt]}>"
 
