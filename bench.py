@@ -300,8 +300,10 @@ def bb_kernel_name(cfg: dict) -> str:
         return f"k_bb_row<{DT_NAME[dt]}, {D}> + k_bb_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32
-        kern = "k_bb_share" if (D <= 64 and nch <= 3) or nch <= 2 else "k_bb_res"  # contiguous: row strides fit
-        return f"{kern}<{DT_NAME[dt]}, {D}, {nch}>"
+        if (D <= 64 and nch <= 3) or nch <= 2:  # contiguous: row strides fit
+            return f"k_bb_share<{DT_NAME[dt]}, {D}, {nch}>"
+        half = int(nch >= 3 and L <= 32 * nch - 16)  # the last chunk holds one 16-row tile
+        return f"k_bb_res<{DT_NAME[dt]}, {D}, {nch}, {half}>"
     return f"k_bb_fused<{DT_NAME[dt]}>"
 
 
@@ -315,8 +317,12 @@ def bwd_kernel_name(cfg: dict) -> str:
         return f"k_bwd_row<{DT_NAME[dt]}, {D}> + k_bwd_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32
-        kern = "k_bwd_pipe" if D <= 64 or nch <= 2 else ("k_bwd_pp" if L <= 112 else "k_bwd_res")
-        return f"{kern}<{DT_NAME[dt]}, {D}, {nch}>"
+        half = int(L <= 32 * nch - 16)  # the last chunk holds one 16-row tile
+        if D <= 64 or nch <= 2:
+            return f"k_bwd_pipe<{DT_NAME[dt]}, {D}, {nch}>"
+        if L <= 112:
+            return f"k_bwd_pp<{DT_NAME[dt]}, {D}, {nch}, {half}>"
+        return f"k_bwd_res<{DT_NAME[dt]}, {D}, {nch}>"
     return f"k_bwd_fused<{DT_NAME[dt]}>"
 
 

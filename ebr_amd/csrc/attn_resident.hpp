@@ -146,6 +146,13 @@ __device__ __forceinline__ void mma_d_sw(f32x4& acc, const unsigned char* region
     }
 }
 
+// Seq-contraction A operand of d tile t for the 16 rows starting at x0, read transposed, for the k = 16 MFMA.
+template <typename T, int DP>
+__device__ __forceinline__ u32x2 seqa_tr16(const unsigned char* region, int x0, int t, const LaneOff<T, DP>& lo) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)(region + x0 * Sw<DP>::ROWB + lo.tr[t]));
+    return __builtin_bit_cast(u32x2, v);
+}
+
 // Seq-contraction A operand of d tile t for the 32 rows starting at x0 (multiple of 32), read transposed.
 template <typename T, int DP>
 __device__ __forceinline__ SeqA<T> seqa_tr(const unsigned char* region, int x0, int t, const LaneOff<T, DP>& lo) {
@@ -709,10 +716,13 @@ template <typename T, int DP, int NCH> struct BwdPP {
     static constexpr bool FITS = SMEM <= 160 * 1024;
 };
 
-template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp_waves(NCH) + 1)) void k_bwd_pp(Args a) {
+// HALF (L <= 32 NCH - 16): the last chunk holds one 16-row tile; rows past it are neither loaded nor read.
+template <typename T, int DP, int NCH, bool HALF>
+__global__ __launch_bounds__(64 * (bwd_pp_waves(NCH) + 1)) void k_bwd_pp(Args a) {
     using LY = Lay<T, DP>;
     using R = BwdPP<T, DP, NCH>;
     constexpr int Lp = R::LP;
+    constexpr int LR = Lp - (HALF ? 16 : 0);  // rows loaded into the regions
     __shared__ __align__(1024) unsigned char smem[R::SMEM];
     unsigned char* Kr = smem;
     unsigned char* Vr = smem + R::RB;
@@ -734,8 +744,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
         }
         auto region2 = [&](unsigned char* r0, const Strided& t0, unsigned char* r1, const Strided& t1, int sl) {
             const int b = sl / a.H, h = sl - b * a.H;
-            async_rows<T, DP>(r0, slice<T>(t0, b, h), t0.sl, L, Lp, 0, 1, w.lane);
-            async_rows<T, DP>(r1, slice<T>(t1, b, h), t1.sl, L, Lp, 0, 1, w.lane);
+            async_rows<T, DP>(r0, slice<T>(t0, b, h), t0.sl, L, LR, 0, 1, w.lane);
+            async_rows<T, DP>(r1, slice<T>(t1, b, h), t1.sl, L, LR, 0, 1, w.lane);
         };
         region2(Kr, a.k, Vr, a.v, s);
         async_wait();
@@ -817,10 +827,11 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
                 constexpr bool LAST = C == NCH - 1;
                 const int x0 = C * CH;
                 f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+                constexpr bool H16 = HALF && LAST;  // keys past LR: no products, P masked to 0 below
                 mma_d_sw<T, DP>(p0, Kr, x0, qf, lo);
-                mma_d_sw<T, DP>(p1, Kr, x0 + 16, qf, lo);
+                if (!H16) mma_d_sw<T, DP>(p1, Kr, x0 + 16, qf, lo);
                 mma_d_sw<T, DP>(d0, Vr, x0, df, lo);
-                mma_d_sw<T, DP>(d1, Vr, x0 + 16, df, lo);
+                if (!H16) mma_d_sw<T, DP>(d1, Vr, x0 + 16, df, lo);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int x = x0 + 4 * w.g + r;
@@ -829,9 +840,15 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
                     d0[r] = p0[r] * (d0[r] - dr);
                     d1[r] = p1[r] * (d1[r] - dr);
                 }
-                const SeqB<T> dsb = make_seqb<T>(d0, d1);
+                if constexpr (H16) {
+                    const u32x2 dsb = pack4<T>(d0);
 #pragma unroll
-                for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, x0, t, lo), dsb);
+                    for (int t = 0; t < LY::NT; ++t) acc[t] = ET<T>::mma16(seqa_tr16<T, DP>(Kr, x0, t, lo), dsb, acc[t]);
+                } else {
+                    const SeqB<T> dsb = make_seqb<T>(d0, d1);
+#pragma unroll
+                    for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Kr, x0, t, lo), dsb);
+                }
             });
             own_from_lds<T, DP>(kf, Kr, row0, lo);
             own_from_lds<T, DP>(vf, Vr, row0, lo);
@@ -852,24 +869,30 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
             SeqB<T> pbs[NCH], dsbs[NCH];
             static_for<0, NCH>([&](auto cc) {
                 constexpr int C = decltype(cc)::value;
+                constexpr bool H16 = HALF && C == NCH - 1;  // query rows past LR: P and dS stay 0
                 const int x0 = C * CH;
                 const f32x4 l0 = *reinterpret_cast<const f32x4*>(l2s + x0 + 4 * w.g);
-                const f32x4 l1 = *reinterpret_cast<const f32x4*>(l2s + x0 + 16 + 4 * w.g);
                 const f32x4 r0 = *reinterpret_cast<const f32x4*>(drs + x0 + 4 * w.g);
-                const f32x4 r1 = *reinterpret_cast<const f32x4*>(drs + x0 + 16 + 4 * w.g);
                 f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
                 mma_d_sw<T, DP>(p0, Qr, x0, kf, lo);
-                mma_d_sw<T, DP>(p1, Qr, x0 + 16, kf, lo);
                 mma_d_sw<T, DP>(d0, Or, x0, vf, lo);
-                mma_d_sw<T, DP>(d1, Or, x0 + 16, vf, lo);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     p0[r] = fast_exp2(fmaf(p0[r], sc2, -l0[r]));  // lse = +inf on padded query rows -> P = 0
-                    p1[r] = fast_exp2(fmaf(p1[r], sc2, -l1[r]));
                     d0[r] = p0[r] * (d0[r] - r0[r]);
-                    d1[r] = p1[r] * (d1[r] - r1[r]);
                 }
-                pbs[C] = make_seqb<T>(p0, p1);
+                if constexpr (!H16) {
+                    const f32x4 l1 = *reinterpret_cast<const f32x4*>(l2s + x0 + 16 + 4 * w.g);
+                    const f32x4 r1 = *reinterpret_cast<const f32x4*>(drs + x0 + 16 + 4 * w.g);
+                    mma_d_sw<T, DP>(p1, Qr, x0 + 16, kf, lo);
+                    mma_d_sw<T, DP>(d1, Or, x0 + 16, vf, lo);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        p1[r] = fast_exp2(fmaf(p1[r], sc2, -l1[r]));
+                        d1[r] = p1[r] * (d1[r] - r1[r]);
+                    }
+                }
+                pbs[C] = make_seqb<T>(p0, p1);  // at H16 only the first half (words 0, 1) is read
                 dsbs[C] = make_seqb<T>(d0, d1);
             });
             constexpr int NH = LY::NT / 2;
@@ -884,8 +907,14 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (bwd_pp
                     const int x0 = C * CH;
 #pragma unroll
                     for (int t = 0; t < NH; ++t) {
-                        av[t] = mma_seq<T>(av[t], seqa_tr<T, DP>(Or, x0, half * NH + t, lo), pbs[C]);
-                        ak[t] = mma_seq<T>(ak[t], seqa_tr<T, DP>(Qr, x0, half * NH + t, lo), dsbs[C]);
+                        if constexpr (HALF && C == NCH - 1) {
+                            const u32x2 pb2 = {pbs[C].v[0], pbs[C].v[1]}, ds2 = {dsbs[C].v[0], dsbs[C].v[1]};
+                            av[t] = ET<T>::mma16(seqa_tr16<T, DP>(Or, x0, half * NH + t, lo), pb2, av[t]);
+                            ak[t] = ET<T>::mma16(seqa_tr16<T, DP>(Qr, x0, half * NH + t, lo), ds2, ak[t]);
+                        } else {
+                            av[t] = mma_seq<T>(av[t], seqa_tr<T, DP>(Or, x0, half * NH + t, lo), pbs[C]);
+                            ak[t] = mma_seq<T>(ak[t], seqa_tr<T, DP>(Qr, x0, half * NH + t, lo), dsbs[C]);
+                        }
                     }
                 });
 #pragma unroll
@@ -920,10 +949,14 @@ template <typename T, int DP, int NCH> struct BbRes {
     static constexpr int SMEM = 4 * RB;  // K, gK, V, gV; later Q, gQ, dO in the same space
 };
 
-template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bb_res(Args a) {
+// HALF: the slice has at most 32 NCH - 16 rows, so the last chunk holds one 16-row tile: rows past it are neither
+// loaded nor read (its d-contractions use one tile, its seq-contractions the k = 16 MFMA), 12.5% fewer score
+// products at NCH = 4.
+template <typename T, int DP, int NCH, bool HALF> __global__ __launch_bounds__(512) void k_bb_res(Args a) {
     using LY = Lay<T, DP>;
     using R = BbRes<T, DP, NCH>;
-    constexpr int Lp = NCH * CH;
+    constexpr int Lp = NCH * CH - (HALF ? 16 : 0);  // rows loaded and read
+    auto live = [](int C, int hh) { return !(HALF && C == NCH - 1 && hh == 1); };  // tile hh of chunk C below Lp
     __shared__ __align__(1024) unsigned char smem[R::SMEM];
     __shared__ __align__(16) float st[4 * STAT_MAX];  // lse * log2 e, Dr, E, T
     const WaveIds w = wave_ids();
@@ -976,6 +1009,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (!live(C, hh)) continue;  // keys past Lp: their P is masked to 0 below
                     const int r0 = x0 + 16 * hh;
                     mma_d_sw<T, DP>(p[hh], Kr, r0, qf, lo);
                     mma_d_sw<T, DP>(at[hh], Kr, r0, gqf, lo);
@@ -1026,10 +1060,18 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 const SeqB<T> peb = pack_seqb<T>(pe);
 #pragma unroll
                 for (int t = 0; t < LY::NT; ++t) {
-                    hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(Kr, x0, t, lo), d2b);
-                    hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, lo), dsb[C]);
-                    hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(Vr, x0, t, lo), peb);
-                    hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, lo), pb[C]);
+                    if constexpr (HALF && C == NCH - 1) {
+                        auto lo2 = [](const SeqB<T>& x) { return u32x2{x.v[0], x.v[1]}; };
+                        hq[t] = ET<T>::mma16(seqa_tr16<T, DP>(Kr, x0, t, lo), lo2(d2b), hq[t]);
+                        hq[t] = ET<T>::mma16(seqa_tr16<T, DP>(gKr, x0, t, lo), lo2(dsb[C]), hq[t]);
+                        hdo[t] = ET<T>::mma16(seqa_tr16<T, DP>(Vr, x0, t, lo), lo2(peb), hdo[t]);
+                        hdo[t] = ET<T>::mma16(seqa_tr16<T, DP>(gVr, x0, t, lo), lo2(pb[C]), hdo[t]);
+                    } else {
+                        hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(Kr, x0, t, lo), d2b);
+                        hq[t] = mma_seq<T>(hq[t], seqa_tr<T, DP>(gKr, x0, t, lo), dsb[C]);
+                        hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(Vr, x0, t, lo), peb);
+                        hdo[t] = mma_seq<T>(hdo[t], seqa_tr<T, DP>(gVr, x0, t, lo), pb[C]);
+                    }
                 }
             });
             if (own < L) {
@@ -1073,6 +1115,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (!live(C, hh)) continue;  // query rows past Lp: their tile values are never read
             const int r0 = x0 + 16 * hh;
             mma_d_sw<T, DP>(p[hh], Qr, r0, kf, lo);
             mma_d_sw<T, DP>(at[hh], Qr, r0, gkf, lo);
@@ -1083,6 +1126,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         f32x4 ds[2], ds2[2], pa[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
+            ds[hh] = ds2[hh] = pa[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (!live(C, hh)) continue;
             const int so = x0 + 16 * hh + 4 * w.g;
             const f32x4 ls = *reinterpret_cast<const f32x4*>(st + so);
             const f32x4 rs = *reinterpret_cast<const f32x4*>(st + STAT_MAX + so);
@@ -1099,14 +1144,24 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 pa[hh][r] = pv * (av - es[r]);
             }
         }
-        const SeqB<T> dsb = make_seqb<T>(ds[0], ds[1]);
-        const SeqB<T> ds2b = make_seqb<T>(ds2[0], ds2[1]);
-        const SeqB<T> pab = make_seqb<T>(pa[0], pa[1]);
+        if constexpr (HALF && C == NCH - 1) {
+            const u32x2 dsb = pack4<T>(ds[0]), ds2b = pack4<T>(ds2[0]), pab = pack4<T>(pa[0]);
 #pragma unroll
-        for (int t = 0; t < LY::NT; ++t) {
-            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, x0, t, lo), ds2b);
-            hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, x0, t, lo), dsb);
-            hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, x0, t, lo), pab);
+            for (int t = 0; t < LY::NT; ++t) {
+                hk[t] = ET<T>::mma16(seqa_tr16<T, DP>(Qr, x0, t, lo), ds2b, hk[t]);
+                hk[t] = ET<T>::mma16(seqa_tr16<T, DP>(gQr, x0, t, lo), dsb, hk[t]);
+                hv[t] = ET<T>::mma16(seqa_tr16<T, DP>(Or, x0, t, lo), pab, hv[t]);
+            }
+        } else {
+            const SeqB<T> dsb = make_seqb<T>(ds[0], ds[1]);
+            const SeqB<T> ds2b = make_seqb<T>(ds2[0], ds2[1]);
+            const SeqB<T> pab = make_seqb<T>(pa[0], pa[1]);
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) {
+                hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(Qr, x0, t, lo), ds2b);
+                hk[t] = mma_seq<T>(hk[t], seqa_tr<T, DP>(gQr, x0, t, lo), dsb);
+                hv[t] = mma_seq<T>(hv[t], seqa_tr<T, DP>(Or, x0, t, lo), pab);
+            }
         }
     });
     if (own < L) {

@@ -51,6 +51,12 @@ template <> struct ET<__bf16> {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0,
                                                        0);
     }
+    // k = 16 (v_mfma_f32_16x16x16_bf16): lane (row or column l16, group g) holds k = 4 g .. 4 g + 3
+    static __device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
+        typedef __attribute__((ext_vector_type(4))) short s4;
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0,
+                                                         0);
+    }
 };
 
 template <> struct ET<_Float16> {
@@ -63,6 +69,9 @@ template <> struct ET<_Float16> {
     static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0,
                                                       0);
+    }
+    static __device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4, a), __builtin_bit_cast(v4, b), c, 0, 0, 0);
     }
 };
 

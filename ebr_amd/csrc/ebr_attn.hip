@@ -965,16 +965,25 @@ template <typename T, int DP> struct BwdLaunch {
                     if (nch == 1) return pipe(std::integral_constant<int, 1>{});
                     if (nch == 2) return pipe(std::integral_constant<int, 2>{});
                     // one K, V and one Q, dO region, each loaded a pass ahead (k_bwd_pp), up to 7 compute waves
-                    auto pp = [&](auto nchc) {
+                    auto pp = [&](auto nchc, auto halfc) {
                         constexpr int N = decltype(nchc)::value;
+                        constexpr bool HALF = decltype(halfc)::value;
                         static_assert(BwdPP<T, DP, N>::FITS, "the two regions and the store areas fit the LDS");
                         const int thr = BwdPP<T, DP, N>::THREADS;
-                        const dim3 pg(persistent_grid(reinterpret_cast<const void*>(k_bwd_pp<T, DP, N>), thr, bh));
-                        hipLaunchKernelGGL((k_bwd_pp<T, DP, N>), pg, dim3(thr), 0, s, a);
+                        const dim3 pg(
+                            persistent_grid(reinterpret_cast<const void*>(k_bwd_pp<T, DP, N, HALF>), thr, bh));
+                        hipLaunchKernelGGL((k_bwd_pp<T, DP, N, HALF>), pg, dim3(thr), 0, s, a);
                         return launch_rc();
                     };
-                    if (nch == 3) return pp(std::integral_constant<int, 3>{});
-                    if (a.L <= 16 * BwdPP<T, DP, 4>::NWC) return pp(std::integral_constant<int, 4>{});
+                    using yes = std::true_type;
+                    using no = std::false_type;
+                    if (nch == 3) {
+                        return a.L <= 3 * CH - 16 ? pp(std::integral_constant<int, 3>{}, yes{})
+                                                  : pp(std::integral_constant<int, 3>{}, no{});
+                    }
+                    // four chunks: 7 compute waves, L <= 112, so the last chunk always holds one 16-row tile
+                    static_assert(16 * BwdPP<T, DP, 4>::NWC == 4 * CH - 16, "HALF at four chunks");
+                    if (a.L <= 16 * BwdPP<T, DP, 4>::NWC) return pp(std::integral_constant<int, 4>{}, yes{});
                 }
                 const dim3 grid((int)bh), block(fused_threads(a.L));
                 switch (nch) {
@@ -1047,11 +1056,18 @@ template <typename T, int DP> struct BbLaunch {
                         if (nch == 3) return share(std::integral_constant<int, 3>{});
                     }
                 }
+                const bool half = a.L <= nch * CH - 16;  // the last chunk holds one 16-row tile
                 switch (nch) {
-                    case 1: hipLaunchKernelGGL((k_bb_res<T, DP, 1>), grid, block, 0, s, a); break;
-                    case 2: hipLaunchKernelGGL((k_bb_res<T, DP, 2>), grid, block, 0, s, a); break;
-                    case 3: hipLaunchKernelGGL((k_bb_res<T, DP, 3>), grid, block, 0, s, a); break;
-                    default: hipLaunchKernelGGL((k_bb_res<T, DP, 4>), grid, block, 0, s, a); break;
+                    case 1: hipLaunchKernelGGL((k_bb_res<T, DP, 1, false>), grid, block, 0, s, a); break;
+                    case 2: hipLaunchKernelGGL((k_bb_res<T, DP, 2, false>), grid, block, 0, s, a); break;
+                    case 3:
+                        if (half) hipLaunchKernelGGL((k_bb_res<T, DP, 3, true>), grid, block, 0, s, a);
+                        else hipLaunchKernelGGL((k_bb_res<T, DP, 3, false>), grid, block, 0, s, a);
+                        break;
+                    default:
+                        if (half) hipLaunchKernelGGL((k_bb_res<T, DP, 4, true>), grid, block, 0, s, a);
+                        else hipLaunchKernelGGL((k_bb_res<T, DP, 4, false>), grid, block, 0, s, a);
+                        break;
                 }
             }
             return launch_rc();
