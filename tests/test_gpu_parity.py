@@ -183,11 +183,16 @@ def test_config4_shape_bf16(cuda):
 # ---------------------------------------------------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("L", [81, 200])
-def test_strided_views(cuda, L):
-    """q, k, v as transposed views of one [B, L, 3, H, D] projection (non-contiguous B/H/L strides)."""
-    B, H, D = 3, 4, 64
-    _say(f"strided qkv views L={L}")
+@pytest.mark.parametrize(
+    "B,L,D",
+    [(3, 81, 64), (3, 200, 64), (3, 45, 128), (3, 70, 128), (70, 100, 128)],
+)
+def test_strided_views(cuda, B, L, D):
+    """q, k, v as transposed views of one [B, L, 3, H, D] projection (non-contiguous B/H/L strides); at D = 128 the
+    persistent backward kernels (k_bwd_pipe, k_bwd_pp) and the half-chunk backward of the backward, B = 70 giving more
+    slices than the persistent grid."""
+    H = 4
+    _say(f"strided qkv views B={B} L={L} D={D}")
     g = torch.Generator().manual_seed(7)
     qkv = (torch.randn(B, L, 3, H, D, generator=g) * 0.125).to(torch.bfloat16)
     do = torch.randn(B, H, L, D, generator=g).to(torch.bfloat16)
@@ -204,7 +209,7 @@ def test_strided_views(cuda, L):
     got = [x.cpu() for x in (o, lse, dq, dk, dv, hq, hk, hv, hdo)]
     qc, kc, vc = (qkv[:, :, i].transpose(1, 2).contiguous() for i in range(3))
     ref = _oracle_all(qc, kc, vc, do, gq, gk, gv, scale, o=got[0], lse=got[1])
-    _compare(got, ref, torch.bfloat16, f"strided L={L}")
+    _compare(got, ref, torch.bfloat16, f"strided B={B} L={L} D={D}")
 
 
 def test_wide_row_stride(cuda):
