@@ -44,6 +44,18 @@ __device__ __forceinline__ void loader_loop(unsigned char* smem, int nst, Issue&
     }
 }
 
+// Stage order of the long kernels. When L is not a multiple of the stage depth, the short last stage (nv rows below
+// L) is taken first, as stage 0, 16 rows at a time as far as L: its 16-row tiles wholly past L are neither multiplied
+// nor read, and the seq-contractions take the k = 16 MFMA (the 30 x 30 grids, L = 900, end in a stage of 4 rows). The
+// full stages follow in order and need no masking. Taken after the loop instead, the tail's code raised the loop's
+// register count (the bwd_bwd col kernel from 128 to 154 VGPRs, one workgroup per CU fewer).
+struct StageOrder {
+    int nfull, rows;
+    bool tail;
+    __device__ __forceinline__ StageOrder(int L, int rows_) : nfull(L / rows_), rows(rows_), tail(L % rows_ != 0) {}
+    __device__ __forceinline__ int row(int i) const { return (tail ? (i == 0 ? nfull : i - 1) : i) * rows; }
+};
+
 // =====================================================================================================================
 // Forward: online softmax over the stages (reference point m in log2 units, running sum l, accumulator rescaled by
 // exp2(m_old - m_new) when m moves).
@@ -60,6 +72,7 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
     const int nst = (L + LSTAGE - 1) / LSTAGE;
+    const StageOrder so(L, LSTAGE);
 
     if (w.wave == NWC) {
         const T* Kg = slice<T>(a.k, b, h);
@@ -67,8 +80,8 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         loader_loop<STB>(
             smem, nst,
             [&](int i, unsigned char* buf) {
-                async_stage<T, DP>(buf, Kg, a.k.sl, L, i * LSTAGE, w.lane);
-                async_stage<T, DP>(buf + C::SB, Vg, a.v.sl, L, i * LSTAGE, w.lane);
+                async_stage<T, DP>(buf, Kg, a.k.sl, L, so.row(i), w.lane);
+                async_stage<T, DP>(buf + C::SB, Vg, a.v.sl, L, so.row(i), w.lane);
             },
             [](int, unsigned char*) {});
         return;
@@ -85,33 +98,11 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
-    for (int i = 0; i < nst; ++i) {
-        lds_barrier();  // stage i in its buffer
-        if (!active) continue;
-        const unsigned char* Kr = smem + (i & 1) * STB;
-        const unsigned char* Vr = Kr + C::SB;
-        const int kb = i * LSTAGE;
-        f32x4 s[4];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            mma_d_sw<T, DP>(s[kt], Kr, 16 * kt, qf, lo);
-        }
-        if (kb + LSTAGE > L) {  // the last stage: keys past L
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (kb + 16 * kt + 4 * w.g + r >= L) s[kt][r] = -INFINITY;
-        }
-        float mx = s[0][0];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int r = (kt == 0 ? 1 : 0); r < 4; ++r) mx = fmax_nn(mx, s[kt][r]);
-        // Every stage holds at least one key below L, so the stage maximum is finite. The reference point m moves
-        // only when some row's maximum exceeds it by more than RESCALE_SLACK (wave vote): P stays <= 2^SLACK, and
-        // the accumulator is rescaled a few times per row instead of at every stage.
+    // Folds a stage's or tile's score maximum mx (-inf past L) into the running reference point m: rescales l and acc
+    // when some row's maximum exceeds m by more than RESCALE_SLACK (wave vote), so P stays <= 2^SLACK and the
+    // accumulator is rescaled a few times per row instead of at every stage. Every stage and tile holds a key below
+    // L, so mx is finite.
+    auto track_max = [&](float mx) {
         const float ms = xmax4(mx) * sc2;
         if (__any(ms > m + RESCALE_SLACK)) {
             const float mn = fmaxf(m, ms);
@@ -121,6 +112,21 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
 #pragma unroll
             for (int t = 0; t < LY::NT; ++t) acc[t] *= alpha;
         }
+    };
+    // A full stage of keys from Kr, Vr (all below L).
+    auto stage = [&](const unsigned char* Kr, const unsigned char* Vr) {
+        f32x4 s[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            mma_d_sw<T, DP>(s[kt], Kr, 16 * kt, qf, lo);
+        }
+        float mx = s[0][0];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = (kt == 0 ? 1 : 0); r < 4; ++r) mx = fmax_nn(mx, s[kt][r]);
+        track_max(mx);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             f32x4 p0 = s[2 * c], p1 = s[2 * c + 1];
@@ -134,6 +140,37 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
 #pragma unroll
             for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Vr, 32 * c, t, lo), pb);
         }
+    };
+    // One 16-key tile of the short stage, keys x0 .. x0 + 15 of Kr, Vr, those at nv and past masked (k = 16 MFMA).
+    auto tile16 = [&](const unsigned char* Kr, const unsigned char* Vr, int x0, int nv) {
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        mma_d_sw<T, DP>(s, Kr, x0, qf, lo);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (x0 + 4 * w.g + r >= nv) s[r] = -INFINITY;
+        track_max(fmax_nn(fmax_nn(s[0], s[1]), fmax_nn(s[2], s[3])));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s[r] = fast_exp2(fmaf(s[r], sc2, -m));
+            l += s[r];
+        }
+        const u32x2 pb = pack4<T>(s);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) acc[t] = ET<T>::mma16(seqa_tr16<T, DP>(Vr, x0, t, lo), pb, acc[t]);
+    };
+    if (so.tail) {
+        lds_barrier();  // stage 0, the short one, in its buffer
+        if (active) {
+            const int nv = L - so.nfull * LSTAGE;
+#pragma nounroll
+            for (int x0 = 0; x0 < nv; x0 += 16) tile16(smem, smem + C::SB, x0, nv);
+        }
+    }
+    for (int i = so.tail ? 1 : 0; i < nst; ++i) {
+        lds_barrier();  // stage i in its buffer
+        if (!active) continue;
+        const unsigned char* Kr = smem + (i & 1) * STB;
+        stage(Kr, Kr + C::SB);
     }
     if (!active) return;
     l = xsum4(l);
@@ -180,6 +217,7 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
     const int nst = (L + LSTAGE - 1) / LSTAGE;
+    const StageOrder so(L, LSTAGE);
 
     if (w.wave == NWC) {
         const T* Kg = slice<T>(a.k, b, h);
@@ -187,8 +225,8 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         loader_loop<STB>(
             smem, nst,
             [&](int i, unsigned char* buf) {
-                async_stage<T, DP>(buf, Kg, a.k.sl, L, i * LSTAGE, w.lane);
-                async_stage<T, DP>(buf + C::SB, Vg, a.v.sl, L, i * LSTAGE, w.lane);
+                async_stage<T, DP>(buf, Kg, a.k.sl, L, so.row(i), w.lane);
+                async_stage<T, DP>(buf + C::SB, Vg, a.v.sl, L, so.row(i), w.lane);
             },
             [](int, unsigned char*) {});
         return;
@@ -210,59 +248,71 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
     f32x4 acc[LY::NT];
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < nst; ++i) {
+    // A full stage of keys from Kr, Vr (all below L).
+    auto stage = [&](const unsigned char* Kr, const unsigned char* Vr) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            f32x4 p[2], dp[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                p[hh] = dp[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                u32x4 ka[LY::NC], va[LY::NC];
+#pragma unroll
+                for (int q = 0; q < LY::NC; ++q) {
+                    const int o = (32 * c + 16 * hh) * Sw<DP>::ROWB + lo.a[q];
+                    ka[q] = *reinterpret_cast<const u32x4*>(Kr + o);
+                    va[q] = *reinterpret_cast<const u32x4*>(Vr + o);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < LY::NC; ++q) {
+                    p[hh] = ET<T>::mma(ka[q], qf.v[q], p[hh]);
+                    dp[hh] = ET<T>::mma(va[q], df.v[q], dp[hh]);
+                }
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
+                    p[hh][r] = pv * (dp[hh][r] - dr);  // dS
+                }
+            const SeqB<T> dsb = make_seqb<T>(p[0], p[1]);
+            SeqA<T> kt[LY::NT];
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) kt[t] = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], kt[t], dsb);
+        }
+    };
+    // One 16-key tile of the short stage, keys x0 .. x0 + 15 of Kr, Vr, those at nv and past masked (k = 16 MFMA).
+    auto tile16 = [&](const unsigned char* Kr, const unsigned char* Vr, int x0, int nv) {
+        f32x4 p = {0.f, 0.f, 0.f, 0.f}, dp = p;
+        mma_d_sw<T, DP>(p, Kr, x0, qf, lo);
+        mma_d_sw<T, DP>(dp, Vr, x0, df, lo);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float pv = x0 + 4 * w.g + r < nv ? fast_exp2(fmaf(p[r], sc2, -lse2)) : 0.f;
+            p[r] = pv * (dp[r] - dr);  // dS
+        }
+        const u32x2 dsb = pack4<T>(p);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) acc[t] = ET<T>::mma16(seqa_tr16<T, DP>(Kr, x0, t, lo), dsb, acc[t]);
+    };
+    if (so.tail) {
+        lds_barrier();  // stage 0, the short one, in its buffer
+        if (active) {
+            const int nv = L - so.nfull * LSTAGE;
+#pragma nounroll
+            for (int x0 = 0; x0 < nv; x0 += 16) tile16(smem, smem + C::SB, x0, nv);
+        }
+    }
+    for (int i = so.tail ? 1 : 0; i < nst; ++i) {
         lds_barrier();  // stage i in its buffer
         if (!active) continue;
         const unsigned char* Kr = smem + (i & 1) * STB;
-        const unsigned char* Vr = Kr + C::SB;
-        const int kb = i * LSTAGE;
-        // Keys past L (zero rows in the stage) are masked in the last stage only: a branch per stage, so that the
-        // other stages carry no compare / select work.
-        auto stage = [&](auto lastc) {
-            constexpr bool LAST = decltype(lastc)::value;
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                f32x4 p[2], dp[2];
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    p[hh] = dp[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    u32x4 ka[LY::NC], va[LY::NC];
-#pragma unroll
-                    for (int q = 0; q < LY::NC; ++q) {
-                        const int o = (32 * c + 16 * hh) * Sw<DP>::ROWB + lo.a[q];
-                        ka[q] = *reinterpret_cast<const u32x4*>(Kr + o);
-                        va[q] = *reinterpret_cast<const u32x4*>(Vr + o);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int q = 0; q < LY::NC; ++q) {
-                        p[hh] = ET<T>::mma(ka[q], qf.v[q], p[hh]);
-                        dp[hh] = ET<T>::mma(va[q], df.v[q], dp[hh]);
-                    }
-                }
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
-                        if constexpr (LAST) {
-                            if (kb + 32 * c + 16 * hh + 4 * w.g + r >= L) pv = 0.f;
-                        }
-                        p[hh][r] = pv * (dp[hh][r] - dr);  // dS
-                    }
-                const SeqB<T> dsb = make_seqb<T>(p[0], p[1]);
-                SeqA<T> kt[LY::NT];
-#pragma unroll
-                for (int t = 0; t < LY::NT; ++t) kt[t] = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], kt[t], dsb);
-            }
-        };
-        if (kb + LSTAGE > L)
-            stage(std::true_type{});
-        else
-            stage(std::false_type{});
+        stage(Kr, Kr + C::SB);
     }
     if (active && own < L) store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * DP, acc, a.scale, DP, w.g);
 }
@@ -282,6 +332,7 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
     const int nst = (L + LSTAGE - 1) / LSTAGE;
+    const StageOrder so(L, LSTAGE);
 
     if (w.wave == NWC) {
         const T* Qg = slice<T>(a.q, b, h);
@@ -290,12 +341,12 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         loader_loop<STB>(
             smem, nst,
             [&](int i, unsigned char* buf) {
-                async_stage<T, DP>(buf, Qg, a.q.sl, L, i * LSTAGE, w.lane);
-                async_stage<T, DP>(buf + C::SB, Og, a.dO.sl, L, i * LSTAGE, w.lane);
-                stt.load(a, bh, i * LSTAGE, w.lane);
+                async_stage<T, DP>(buf, Qg, a.q.sl, L, so.row(i), w.lane);
+                async_stage<T, DP>(buf + C::SB, Og, a.dO.sl, L, so.row(i), w.lane);
+                stt.load(a, bh, so.row(i), w.lane);
             },
             [&](int i, unsigned char* buf) {
-                stt.put(reinterpret_cast<float*>(buf + 2 * C::SB), i * LSTAGE, L, w.lane);
+                stt.put(reinterpret_cast<float*>(buf + 2 * C::SB), so.row(i), L, w.lane);
             });
         return;
     }
@@ -311,12 +362,8 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
     f32x4 ak[LY::NT], av[LY::NT];
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) ak[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < nst; ++i) {
-        lds_barrier();  // stage i in its buffer
-        if (!active) continue;
-        const unsigned char* Qr = smem + (i & 1) * STB;
-        const unsigned char* Or = Qr + C::SB;  // dO
-        const float* st = reinterpret_cast<const float*>(Qr + 2 * C::SB);
+    // A full stage of query rows from Qr, Or (dO) with their statistics st (all rows below L).
+    auto stage = [&](const unsigned char* Qr, const unsigned char* Or, const float* st) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             f32x4 p[2], dp[2];
@@ -344,8 +391,8 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
                 const f32x4 d2 = *reinterpret_cast<const f32x4*>(st + LSTAGE + x);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    p[hh][r] = fast_exp2(fmaf(p[hh][r], sc2, -l2[r]));  // lse = +inf past L: P = 0
-                    dp[hh][r] = p[hh][r] * (dp[hh][r] - d2[r]);          // dS
+                    p[hh][r] = fast_exp2(fmaf(p[hh][r], sc2, -l2[r]));
+                    dp[hh][r] = p[hh][r] * (dp[hh][r] - d2[r]);  // dS
                 }
             }
             const SeqB<T> pb = make_seqb<T>(p[0], p[1]);
@@ -359,6 +406,41 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
                 ak[t] = mma_seq<T>(ak[t], qt, dsb);
             }
         }
+    };
+    // One 16-row tile of the short stage, rows x0 .. x0 + 15 (k = 16 MFMA); rows past L carry lse = +inf: P = 0.
+    auto tile16 = [&](const unsigned char* Qr, const unsigned char* Or, const float* st, int x0) {
+        f32x4 p = {0.f, 0.f, 0.f, 0.f}, dp = p;
+        mma_d_sw<T, DP>(p, Qr, x0, kf, lo);
+        mma_d_sw<T, DP>(dp, Or, x0, vf, lo);
+        const f32x4 l2 = *reinterpret_cast<const f32x4*>(st + x0 + 4 * w.g);
+        const f32x4 d2 = *reinterpret_cast<const f32x4*>(st + LSTAGE + x0 + 4 * w.g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = fast_exp2(fmaf(p[r], sc2, -l2[r]));
+            dp[r] = p[r] * (dp[r] - d2[r]);  // dS
+        }
+        const u32x2 pb = pack4<T>(p);
+        const u32x2 dsb = pack4<T>(dp);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            av[t] = ET<T>::mma16(seqa_tr16<T, DP>(Or, x0, t, lo), pb, av[t]);
+            ak[t] = ET<T>::mma16(seqa_tr16<T, DP>(Qr, x0, t, lo), dsb, ak[t]);
+        }
+    };
+    if (so.tail) {
+        lds_barrier();  // stage 0, the short one, in its buffer
+        if (active) {
+            const int nv = L - so.nfull * LSTAGE;
+#pragma nounroll
+            for (int x0 = 0; x0 < nv; x0 += 16)
+                tile16(smem, smem + C::SB, reinterpret_cast<const float*>(smem + 2 * C::SB), x0);
+        }
+    }
+    for (int i = so.tail ? 1 : 0; i < nst; ++i) {
+        lds_barrier();  // stage i in its buffer
+        if (!active) continue;
+        const unsigned char* Qr = smem + (i & 1) * STB;
+        stage(Qr, Qr + C::SB, reinterpret_cast<const float*>(Qr + 2 * C::SB));
     }
     if (active && own < L) {
         const int64_t r = ((int64_t)bh * L + own) * DP;
@@ -388,6 +470,7 @@ __global__ __launch_bounds__(64 * (NWC + 1)) void k_bb_long_row(Args a) {
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
     const int nst = (L + STG - 1) / STG;
+    const StageOrder so(L, STG);
 
     if (w.wave == NWC) {
         const T* Kg = slice<T>(a.k, b, h);
@@ -397,7 +480,7 @@ __global__ __launch_bounds__(64 * (NWC + 1)) void k_bb_long_row(Args a) {
         loader_loop<STB>(
             smem, nst,
             [&](int i, unsigned char* buf) {
-                const int r0 = i * STG;
+                const int r0 = so.row(i);
                 async_rows<T, DP>(buf, Kg + (int64_t)r0 * a.k.sl, a.k.sl, L - r0, STG, 0, 1, w.lane);
                 async_rows<T, DP>(buf + SB, gKg + (int64_t)r0 * a.gk.sl, a.gk.sl, L - r0, STG, 0, 1, w.lane);
                 async_rows<T, DP>(buf + 2 * SB, Vg + (int64_t)r0 * a.v.sl, a.v.sl, L - r0, STG, 0, 1, w.lane);
@@ -428,99 +511,129 @@ __global__ __launch_bounds__(64 * (NWC + 1)) void k_bb_long_row(Args a) {
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) X[t] = U[t] = Z[t] = W[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     float e_acc = 0.f, t_acc = 0.f;
-    for (int i = 0; i < nst; ++i) {
-        lds_barrier();  // stage i in its buffer
-        if (!active) continue;
-        const unsigned char* Kr = smem + (i & 1) * STB;
+    // One 16-key tile's products and statistics: p, at, dp, bm hold S, A, dP, Bm on entry (accumulator layout) and
+    // P, PA, dS, M1 on return, with E and T accumulated. ``live`` masks keys past L (short stage only).
+    auto elementwise = [&](f32x4& p, f32x4& at, f32x4& dp, f32x4& bm, auto live) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float pv = live(r) ? fast_exp2(fmaf(p[r], sc2, -lse2)) : 0.f;
+            const float dsv = pv * (dp[r] - dr);
+            const float av = at[r] * sc;
+            const float pa = pv * av;
+            const float m1 = fmaf(dsv, av, pv * bm[r]);
+            e_acc += pa;
+            t_acc += m1;
+            p[r] = pv;
+            dp[r] = dsv;
+            at[r] = pa;
+            bm[r] = m1;
+        }
+    };
+    // A full stage of keys from the K, gK, V, gV regions at Kr (all below L).
+    auto stage = [&](const unsigned char* Kr) {
         const unsigned char* gKr = Kr + SB;
         const unsigned char* Vr = Kr + 2 * SB;
         const unsigned char* gVr = Kr + 3 * SB;
-        const int kb = i * STG;
-        // Keys past L are masked in the last stage only (a branch per stage, no compare / select work elsewhere).
-        auto stage = [&](auto lastc) {
-            constexpr bool LAST = decltype(lastc)::value;
 #pragma unroll
-            for (int c = 0; c < STG / CH; ++c) {
-                f32x4 p[2], at[2], dp[2], bm[2];
+        for (int c = 0; c < STG / CH; ++c) {
+            f32x4 p[2], at[2], dp[2], bm[2];
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    p[hh] = at[hh] = dp[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    const int r0 = 32 * c + 16 * hh;
-                    {
-                        u32x4 ka[LY::NC], gka[LY::NC];
+            for (int hh = 0; hh < 2; ++hh) {
+                p[hh] = at[hh] = dp[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int r0 = 32 * c + 16 * hh;
+                {
+                    u32x4 ka[LY::NC], gka[LY::NC];
 #pragma unroll
-                        for (int q = 0; q < LY::NC; ++q) {
-                            const int o = r0 * Sw<DP>::ROWB + lo.a[q];
-                            ka[q] = *reinterpret_cast<const u32x4*>(Kr + o);
-                            gka[q] = *reinterpret_cast<const u32x4*>(gKr + o);
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                        for (int q = 0; q < LY::NC; ++q) {
-                            p[hh] = ET<T>::mma(ka[q], qf.v[q], p[hh]);
-                            at[hh] = ET<T>::mma(ka[q], gqf.v[q], at[hh]);
-                            at[hh] = ET<T>::mma(gka[q], qf.v[q], at[hh]);
-                        }
+                    for (int q = 0; q < LY::NC; ++q) {
+                        const int o = r0 * Sw<DP>::ROWB + lo.a[q];
+                        ka[q] = *reinterpret_cast<const u32x4*>(Kr + o);
+                        gka[q] = *reinterpret_cast<const u32x4*>(gKr + o);
                     }
-                    {
-                        u32x4 va[LY::NC], gva[LY::NC];
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                        for (int q = 0; q < LY::NC; ++q) {
-                            const int o = r0 * Sw<DP>::ROWB + lo.a[q];
-                            va[q] = *reinterpret_cast<const u32x4*>(Vr + o);
-                            gva[q] = *reinterpret_cast<const u32x4*>(gVr + o);
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                        for (int q = 0; q < LY::NC; ++q) {
-                            dp[hh] = ET<T>::mma(va[q], df.v[q], dp[hh]);
-                            bm[hh] = ET<T>::mma(gva[q], df.v[q], bm[hh]);
-                        }
+                    for (int q = 0; q < LY::NC; ++q) {
+                        p[hh] = ET<T>::mma(ka[q], qf.v[q], p[hh]);
+                        at[hh] = ET<T>::mma(ka[q], gqf.v[q], at[hh]);
+                        at[hh] = ET<T>::mma(gka[q], qf.v[q], at[hh]);
                     }
                 }
+                {
+                    u32x4 va[LY::NC], gva[LY::NC];
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        float pv = fast_exp2(fmaf(p[hh][r], sc2, -lse2));
-                        if constexpr (LAST) {
-                            if (kb + 32 * c + 16 * hh + 4 * w.g + r >= L) pv = 0.f;
-                        }
-                        const float dsv = pv * (dp[hh][r] - dr);
-                        const float av = at[hh][r] * sc;
-                        const float pa = pv * av;
-                        const float m1 = fmaf(dsv, av, pv * bm[hh][r]);
-                        e_acc += pa;
-                        t_acc += m1;
-                        p[hh][r] = pv;
-                        dp[hh][r] = dsv;
-                        at[hh][r] = pa;
-                        bm[hh][r] = m1;
+                    for (int q = 0; q < LY::NC; ++q) {
+                        const int o = r0 * Sw<DP>::ROWB + lo.a[q];
+                        va[q] = *reinterpret_cast<const u32x4*>(Vr + o);
+                        gva[q] = *reinterpret_cast<const u32x4*>(gVr + o);
                     }
-                const SeqB<T> pb = make_seqb<T>(p[0], p[1]);
-                const SeqB<T> dsb = make_seqb<T>(dp[0], dp[1]);
-                const SeqB<T> pab = make_seqb<T>(at[0], at[1]);
-                const SeqB<T> m1b = make_seqb<T>(bm[0], bm[1]);
-#pragma unroll
-                for (int t = 0; t < LY::NT; ++t) {
-                    const SeqA<T> kt = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
-                    const SeqA<T> gkt = seqa_tr<T, DP>(gKr, 32 * c, t, lo);
-                    const SeqA<T> vt = seqa_tr<T, DP>(Vr, 32 * c, t, lo);
-                    const SeqA<T> gvt = seqa_tr<T, DP>(gVr, 32 * c, t, lo);
                     __builtin_amdgcn_sched_barrier(0);
-                    X[t] = mma_seq<T>(X[t], kt, m1b);
-                    X[t] = mma_seq<T>(X[t], gkt, dsb);
-                    U[t] = mma_seq<T>(U[t], kt, dsb);
-                    Z[t] = mma_seq<T>(Z[t], kt, pb);
-                    W[t] = mma_seq<T>(W[t], vt, pab);
-                    W[t] = mma_seq<T>(W[t], gvt, pb);
+#pragma unroll
+                    for (int q = 0; q < LY::NC; ++q) {
+                        dp[hh] = ET<T>::mma(va[q], df.v[q], dp[hh]);
+                        bm[hh] = ET<T>::mma(gva[q], df.v[q], bm[hh]);
+                    }
                 }
             }
-        };
-        if (kb + STG > L)
-            stage(std::true_type{});
-        else
-            stage(std::false_type{});
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) elementwise(p[hh], at[hh], dp[hh], bm[hh], [](int) { return true; });
+            const SeqB<T> pb = make_seqb<T>(p[0], p[1]);
+            const SeqB<T> dsb = make_seqb<T>(dp[0], dp[1]);
+            const SeqB<T> pab = make_seqb<T>(at[0], at[1]);
+            const SeqB<T> m1b = make_seqb<T>(bm[0], bm[1]);
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) {
+                const SeqA<T> kt = seqa_tr<T, DP>(Kr, 32 * c, t, lo);
+                const SeqA<T> gkt = seqa_tr<T, DP>(gKr, 32 * c, t, lo);
+                const SeqA<T> vt = seqa_tr<T, DP>(Vr, 32 * c, t, lo);
+                const SeqA<T> gvt = seqa_tr<T, DP>(gVr, 32 * c, t, lo);
+                __builtin_amdgcn_sched_barrier(0);
+                X[t] = mma_seq<T>(X[t], kt, m1b);
+                X[t] = mma_seq<T>(X[t], gkt, dsb);
+                U[t] = mma_seq<T>(U[t], kt, dsb);
+                Z[t] = mma_seq<T>(Z[t], kt, pb);
+                W[t] = mma_seq<T>(W[t], vt, pab);
+                W[t] = mma_seq<T>(W[t], gvt, pb);
+            }
+        }
+    };
+    // One 16-key tile of the short stage, keys x0 .. x0 + 15, those at nv and past masked (k = 16 MFMA).
+    auto tile16 = [&](const unsigned char* Kr, int x0, int nv) {
+        const unsigned char* gKr = Kr + SB;
+        const unsigned char* Vr = Kr + 2 * SB;
+        const unsigned char* gVr = Kr + 3 * SB;
+        f32x4 p = {0.f, 0.f, 0.f, 0.f}, at = p, dp = p, bm = p;
+        mma_d_sw<T, DP>(p, Kr, x0, qf, lo);
+        mma_d_sw<T, DP>(at, Kr, x0, gqf, lo);
+        mma_d_sw<T, DP>(at, gKr, x0, qf, lo);
+        mma_d_sw<T, DP>(dp, Vr, x0, df, lo);
+        mma_d_sw<T, DP>(bm, gVr, x0, df, lo);
+        elementwise(p, at, dp, bm, [&](int r) { return x0 + 4 * w.g + r < nv; });
+        const u32x2 pb = pack4<T>(p);
+        const u32x2 dsb = pack4<T>(dp);
+        const u32x2 pab = pack4<T>(at);
+        const u32x2 m1b = pack4<T>(bm);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            const u32x2 kt = seqa_tr16<T, DP>(Kr, x0, t, lo);
+            X[t] = ET<T>::mma16(kt, m1b, X[t]);
+            X[t] = ET<T>::mma16(seqa_tr16<T, DP>(gKr, x0, t, lo), dsb, X[t]);
+            U[t] = ET<T>::mma16(kt, dsb, U[t]);
+            Z[t] = ET<T>::mma16(kt, pb, Z[t]);
+            W[t] = ET<T>::mma16(seqa_tr16<T, DP>(Vr, x0, t, lo), pab, W[t]);
+            W[t] = ET<T>::mma16(seqa_tr16<T, DP>(gVr, x0, t, lo), pb, W[t]);
+        }
+    };
+    if (so.tail) {
+        lds_barrier();  // stage 0, the short one, in its buffer
+        if (active) {
+            const int nv = L - so.nfull * STG;
+#pragma nounroll
+            for (int x0 = 0; x0 < nv; x0 += 16) tile16(smem, x0, nv);
+        }
+    }
+    for (int i = so.tail ? 1 : 0; i < nst; ++i) {
+        lds_barrier();  // stage i in its buffer
+        if (!active) continue;
+        stage(smem + (i & 1) * STB);
     }
     if (!active) return;
     const float E = xsum4(e_acc);
@@ -559,6 +672,7 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
     const int b = bh / a.H, h = bh - b * a.H;
     const int L = a.L;
     const int nst = (L + LSTAGE - 1) / LSTAGE;
+    const StageOrder so(L, LSTAGE);
 
     if (w.wave == NWC) {
         const T* Qg = slice<T>(a.q, b, h);
@@ -568,14 +682,14 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         loader_loop<STB>(
             smem, nst,
             [&](int i, unsigned char* buf) {
-                const int r0 = i * LSTAGE;
+                const int r0 = so.row(i);
                 async_stage<T, DP>(buf, Qg, a.q.sl, L, r0, w.lane);
                 async_stage<T, DP>(buf + C::SB, gQg, a.gq.sl, L, r0, w.lane);
                 async_stage<T, DP>(buf + 2 * C::SB, Og, a.dO.sl, L, r0, w.lane);
                 stt.load(a, bh, r0, w.lane);
             },
             [&](int i, unsigned char* buf) {
-                stt.put(reinterpret_cast<float*>(buf + 3 * C::SB), i * LSTAGE, L, w.lane);
+                stt.put(reinterpret_cast<float*>(buf + 3 * C::SB), so.row(i), L, w.lane);
             });
         return;
     }
@@ -594,7 +708,55 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
     f32x4 hk[LY::NT], hv[LY::NT];
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) hk[t] = hv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < nst; ++i) {
+    // One 16-row tile's dS2, dS and Pa from its products (accumulator layout: p, at, dp, bm hold S, A, dP, Bm on
+    // entry; dS2, Pa, dS on return in p, at, dp) and the statistics of its rows at st + x.
+    // With E and T known, dS2 = dS (A - E) + P (Bm - T) and Pa = P (A - E): the centred forms of
+    // dS o A + P o Bm - E dS - T P and P o A - E P, two VALU operations fewer per element.
+    auto elementwise = [&](f32x4& p, f32x4& at, f32x4& dp, const f32x4& bm, const float* st, int x) {
+        const f32x4 l2 = *reinterpret_cast<const f32x4*>(st + x);
+        const f32x4 d2 = *reinterpret_cast<const f32x4*>(st + LSTAGE + x);
+        const f32x4 e2 = *reinterpret_cast<const f32x4*>(st + 2 * LSTAGE + x);
+        const f32x4 t2 = *reinterpret_cast<const f32x4*>(st + 3 * LSTAGE + x);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float pv = fast_exp2(fmaf(p[r], sc2, -l2[r]));  // lse = +inf past L: P = 0
+            const float dsv = pv * (dp[r] - d2[r]);
+            const float ae = fmaf(at[r], sc, -e2[r]);
+            p[r] = fmaf(dsv, ae, pv * (bm[r] - t2[r]));  // dS2
+            dp[r] = dsv;
+            at[r] = pv * ae;  // Pa
+        }
+    };
+    // One 16-row tile of the short stage, rows x0 .. x0 + 15 (k = 16 MFMA).
+    auto tile16 = [&](const unsigned char* Qr, const float* st, int x0) {
+        const unsigned char* gQr = Qr + C::SB;
+        const unsigned char* Or = Qr + 2 * C::SB;
+        f32x4 p = {0.f, 0.f, 0.f, 0.f}, at = p, dp = p, bm = p;
+        mma_d_sw<T, DP>(p, Qr, x0, kf, lo);
+        mma_d_sw<T, DP>(at, gQr, x0, kf, lo);
+        mma_d_sw<T, DP>(at, Qr, x0, gkf, lo);
+        mma_d_sw<T, DP>(dp, Or, x0, vf, lo);
+        mma_d_sw<T, DP>(bm, Or, x0, gvf, lo);
+        elementwise(p, at, dp, bm, st, x0 + 4 * w.g);
+        const u32x2 d2b = pack4<T>(p);
+        const u32x2 dsb = pack4<T>(dp);
+        const u32x2 peb = pack4<T>(at);
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) {
+            hk[t] = ET<T>::mma16(seqa_tr16<T, DP>(Qr, x0, t, lo), d2b, hk[t]);
+            hk[t] = ET<T>::mma16(seqa_tr16<T, DP>(gQr, x0, t, lo), dsb, hk[t]);
+            hv[t] = ET<T>::mma16(seqa_tr16<T, DP>(Or, x0, t, lo), peb, hv[t]);
+        }
+    };
+    if (so.tail) {
+        lds_barrier();  // stage 0, the short one, in its buffer
+        if (active) {
+            const int nv = L - so.nfull * LSTAGE;
+#pragma nounroll
+            for (int x0 = 0; x0 < nv; x0 += 16) tile16(smem, reinterpret_cast<const float*>(smem + 3 * C::SB), x0);
+        }
+    }
+    for (int i = so.tail ? 1 : 0; i < nst; ++i) {
         lds_barrier();  // stage i in its buffer
         if (!active) continue;
         const unsigned char* Qr = smem + (i & 1) * STB;
@@ -637,24 +799,7 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
                 }
             }
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int x = 32 * c + 16 * hh + 4 * w.g;
-                const f32x4 l2 = *reinterpret_cast<const f32x4*>(st + x);
-                const f32x4 d2 = *reinterpret_cast<const f32x4*>(st + LSTAGE + x);
-                const f32x4 e2 = *reinterpret_cast<const f32x4*>(st + 2 * LSTAGE + x);
-                const f32x4 t2 = *reinterpret_cast<const f32x4*>(st + 3 * LSTAGE + x);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    // With E and T known, dS2 = dS (A - E) + P (Bm - T) and Pa = P (A - E): the centred forms of
-                    // dS o A + P o Bm - E dS - T P and P o A - E P, two VALU operations fewer per element.
-                    const float pv = fast_exp2(fmaf(p[hh][r], sc2, -l2[r]));  // lse = +inf past L: P = 0
-                    const float dsv = pv * (dp[hh][r] - d2[r]);
-                    const float ae = fmaf(at[hh][r], sc, -e2[r]);
-                    p[hh][r] = fmaf(dsv, ae, pv * (bm[hh][r] - t2[r]));  // dS2
-                    dp[hh][r] = dsv;
-                    at[hh][r] = pv * ae;  // Pa
-                }
-            }
+            for (int hh = 0; hh < 2; ++hh) elementwise(p[hh], at[hh], dp[hh], bm[hh], st, 32 * c + 16 * hh + 4 * w.g);
             const SeqB<T> d2b = make_seqb<T>(p[0], p[1]);
             const SeqB<T> dsb = make_seqb<T>(dp[0], dp[1]);
             const SeqB<T> peb = make_seqb<T>(at[0], at[1]);

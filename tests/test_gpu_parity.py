@@ -103,6 +103,14 @@ def test_long_L(cuda, L, dtype):
     _case(2, 2, L, 64, dtype, cuda, seed=L)
 
 
+# The long kernels run the last 64-row stage of a slice 16 rows at a time, as far as L: 1, 2, 3 and 4 live tiles
+# (L mod 64 = 22, 33, 49, 63), at every head dim the 16-bit long kernels are built for.
+@pytest.mark.parametrize("L", [150, 161, 177, 191])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_long_last_stage_tiles(cuda, L, D):
+    _case(2, 2, L, D, torch.bfloat16, cuda, seed=L + D)
+
+
 @pytest.mark.parametrize("D", [16, 32, 48, 128])
 @pytest.mark.parametrize("L", [45, 150])
 def test_head_dims_fp32(cuda, D, L):
@@ -166,10 +174,19 @@ def test_config2_maze_bf16_full_size(cuda):
     _sampled(64, 8, 900, 64, torch.bfloat16, cuda, 12)
 
 
-@pytest.mark.parametrize("B,H,L,D,dtype", [(64, 8, 333, 32, torch.bfloat16), (48, 8, 517, 64, torch.float16)])
+@pytest.mark.parametrize(
+    "B,H,L,D,dtype",
+    [
+        (64, 8, 333, 32, torch.bfloat16),
+        (48, 8, 517, 64, torch.float16),
+        (64, 8, 177, 64, torch.bfloat16),
+        (64, 8, 161, 128, torch.bfloat16),
+    ],
+)
 def test_long_wide_grids_ragged_L(cuda, B, H, L, D, dtype):
     """Grids large enough for the wide long-sequence workgroups (7 compute waves; 10 in the bwd_bwd row kernel, with
-    its own 160-row blocking), L not a multiple of any block or stage; 8 random slices checked."""
+    its own 160-row blocking), L not a multiple of any block or stage (last stages of 1 to 4 live 16-row tiles); 8
+    random slices checked."""
     _sampled(B, H, L, D, dtype, cuda, 8, seed=L)
 
 
