@@ -161,6 +161,24 @@ def test_argument_errors():
     assert ops.default_scale(q, None) == 8**-0.5 and ops.default_scale(q, 0.3) == 0.3
 
 
+def test_launcher_argument_errors():
+    """The launcher layer checks its arguments as reference triton_kernels._cfg does (TypeError for a dtype without
+    kernels, ValueError for a tensor that is not 4-D or an unknown input_precision), and takes GPU tensors only; all
+    of it before any launch."""
+    from ebr_amd.fused_attn import kernels
+
+    q = torch.zeros(1, 2, 3, 8)
+    with pytest.raises(TypeError):
+        kernels.attn_fwd(q.to(torch.int32), q, q, 0.5)
+    with pytest.raises(ValueError):
+        kernels.attn_fwd(q[0], q[0], q[0], 0.5)
+    with pytest.raises(ValueError, match="input_precision"):
+        kernels.attn_bwd(q, q, q, q, q[..., 0], q, 0.5, input_precision="fp16")
+    for prec in kernels.PRECISIONS + (None,):
+        with pytest.raises(ValueError, match="GPU tensors"):  # every name the reference accepts passes the check
+            kernels.attn_bwd_bwd(q, q, q, q, q[..., 0], q, None, None, None, None, 0.5, input_precision=prec)
+
+
 def test_rows_keeps_aligned_views_and_copies_others():
     x = torch.zeros(2, 5, 3, 4, 64, dtype=torch.bfloat16)  # [B, L, 3, H, D] projection
     q = x[:, :, 0].transpose(1, 2)

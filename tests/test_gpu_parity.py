@@ -391,3 +391,56 @@ def test_bad_arguments_raise(cuda):
         x = torch.randn(1, 1, 4, 0, device=cuda)
         torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
     assert math.isfinite(1.0)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# Launcher keywords (reference triton_kernels.py:15-17, 566-591)
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("L", [81, 200])
+def test_launcher_lowp_dots(cuda, L):
+    """``kernels.attn_*`` on bf16 inputs. lowp_dots=True (the default) is the ops' path, bit for bit. lowp_dots=False
+    keeps the derived tiles in fp32: each output is then the oracle's fp32 result on the same bf16 values, rounded
+    once to bf16, so it lies within one bf16 step (2^-7 of the largest output) of the oracle, well inside the 2e-2
+    bar of the 16-bit tiles; lse is fp32 and within the fp32 bar."""
+    from ebr_amd.fused_attn import kernels
+
+    B, H, D = 2, 2, 64
+    _say(f"launcher lowp_dots L={L}")
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, torch.bfloat16, seed=L)
+    scale = D**-0.5
+    qd, kd, vd, dod, gqd, gkd, gvd = (x.to(cuda) for x in (q, k, v, do, gq, gk, gv))
+
+    def run(**kw):
+        o, lse = kernels.attn_fwd(qd, kd, vd, scale, **kw)
+        dq, dk, dv = kernels.attn_bwd(qd, kd, vd, o, lse, dod, scale, **kw)
+        hs = kernels.attn_bwd_bwd(qd, kd, vd, o, lse, dod, dq, gqd, gkd, gvd, scale, **kw)
+        torch.cuda.synchronize()
+        return [x.cpu() for x in (o, lse, dq, dk, dv, *hs)]
+
+    ops_path = _hip_all(q, k, v, do, gq, gk, gv, scale, cuda)
+    for a, b in zip(run(), ops_path):
+        assert torch.equal(a, b)
+    wide = run(lowp_dots=False)
+    assert all(t.dtype == (torch.float32 if n == "lse" else torch.bfloat16) for n, t in zip(NAMES, wide))
+    ref = _oracle_all(q, k, v, do, gq, gk, gv, scale, o=wide[0], lse=wide[1])
+    errs = {n: oracle.rel_err(g, r) for n, g, r in zip(NAMES, wide, ref)}
+    print(f"lowp_dots=False L={L}: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    assert errs["lse"] <= TOL[torch.float32] and all(e <= 2.0**-7 for n, e in errs.items() if n != "lse"), errs
+
+
+def test_launcher_input_precision_fp32(cuda):
+    """Every input_precision the reference accepts runs the same IEEE fp32 dots on gfx950: identical outputs."""
+    from ebr_amd.fused_attn import kernels
+
+    _say("launcher input_precision fp32")
+    q, k, v, do, gq, gk, gv = (x.to(cuda) for x in _inputs(2, 2, 64, 64, torch.float32, seed=5))
+    outs = []
+    for prec in kernels.PRECISIONS:
+        o, lse = kernels.attn_fwd(q, k, v, 0.125, input_precision=prec)
+        dq, dk, dv = kernels.attn_bwd(q, k, v, o, lse, do, 0.125, input_precision=prec)
+        hs = kernels.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, None, gv, 0.125, input_precision=prec)
+        outs.append([x.cpu() for x in (o, lse, dq, dk, dv, *hs)])
+    for other in outs[1:]:
+        assert all(torch.equal(a, b) for a, b in zip(outs[0], other))
