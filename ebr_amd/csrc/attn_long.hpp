@@ -16,7 +16,11 @@
 // forward keeps the compiler's order: the extra registers cost it a wave per SIMD and 6%.
 
 constexpr int LSTAGE = 64;  // other-side rows per stage: two 32-row MFMA k-chunks
-constexpr float RESCALE_SLACK = 8.f;  // online softmax: headroom (log2 units) before the running maximum moves
+// Online softmax of the long forward: the exponentials of a stage are taken against the current reference point m
+// first, and accepted when every row's sum of them stays at most stage_sum_max (so each P is at most that, inside
+// the range of the MFMA operand type: 2^32 for bf16, 2^15 for fp16, whose largest value is 65504); otherwise m moves
+// to the row maximum and the stage is redone.
+template <typename T> constexpr float stage_sum_max() { return std::is_same_v<T, _Float16> ? 32768.f : 4294967296.f; }
 
 template <typename T, int DP, int NWC> struct LongCfg {
     static constexpr int SB = LSTAGE * Sw<DP>::ROWB;  // one tensor's stage (bytes)
@@ -97,23 +101,29 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
     f32x4 acc[LY::NT];
 #pragma unroll
     for (int t = 0; t < LY::NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // m: the row's reference point (log2 units); l: the row's sum of P, in every lane of the row. Row sums come from
+    // an MFMA with an all-ones A operand, as the products of the rounded P that also enter P V, so no lane sums.
     float m = -INFINITY, l = 0.f;
-    // Folds a stage's or tile's score maximum mx (-inf past L) into the running reference point m: rescales l and acc
-    // when some row's maximum exceeds m by more than RESCALE_SLACK (wave vote), so P stays <= 2^SLACK and the
-    // accumulator is rescaled a few times per row instead of at every stage. Every stage and tile holds a key below
-    // L, so mx is finite.
-    auto track_max = [&](float mx) {
-        const float ms = xmax4(mx) * sc2;
-        if (__any(ms > m + RESCALE_SLACK)) {
-            const float mn = fmaxf(m, ms);
-            const float alpha = fast_exp2(m - mn);
-            m = mn;
-            l *= alpha;
+    SeqA<T> ones;
+    {
+        typename ET<T>::v8 o;
 #pragma unroll
-            for (int t = 0; t < LY::NT; ++t) acc[t] *= alpha;
-        }
+        for (int e = 0; e < 8; ++e) o[e] = (T)1.f;
+        ones.v = __builtin_bit_cast(u32x4, o);
+    }
+    // Moves m to the row maximum of scores mx (-inf past L; every stage and tile holds a key below L, so it is finite)
+    // where that exceeds m, rescaling l and acc.
+    auto raise_m = [&](float mx) {
+        const float mn = fmaxf(m, xmax4(mx) * sc2);
+        const float alpha = fast_exp2(m - mn);  // 0 while m = -inf (l and acc are still 0)
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int t = 0; t < LY::NT; ++t) acc[t] *= alpha;
     };
-    // A full stage of keys from Kr, Vr (all below L).
+    // A full stage of keys from Kr, Vr (all below L). The common case issues no maximum at all: exponentials against
+    // m, the row sums by MFMA, one vote. The maximum is taken only when a row's sum exceeds stage_sum_max (or is not
+    // finite, as in a first stage with m = -inf).
     auto stage = [&](const unsigned char* Kr, const unsigned char* Vr) {
         f32x4 s[4];
 #pragma unroll
@@ -121,40 +131,51 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
             s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
             mma_d_sw<T, DP>(s[kt], Kr, 16 * kt, qf, lo);
         }
-        float mx = s[0][0];
+        SeqB<T> pb[2];
+        f32x4 ls;
+        auto exps = [&]() {
+            ls = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+            for (int c = 0; c < 2; ++c) {
+                f32x4 p0, p1;
 #pragma unroll
-            for (int r = (kt == 0 ? 1 : 0); r < 4; ++r) mx = fmax_nn(mx, s[kt][r]);
-        track_max(mx);
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            f32x4 p0 = s[2 * c], p1 = s[2 * c + 1];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                p0[r] = fast_exp2(fmaf(p0[r], sc2, -m));
-                p1[r] = fast_exp2(fmaf(p1[r], sc2, -m));
-                l += p0[r] + p1[r];
+                for (int r = 0; r < 4; ++r) {
+                    p0[r] = fast_exp2(fmaf(s[2 * c][r], sc2, -m));
+                    p1[r] = fast_exp2(fmaf(s[2 * c + 1][r], sc2, -m));
+                }
+                pb[c] = make_seqb<T>(p0, p1);
+                ls = mma_seq<T>(ls, ones, pb[c]);
             }
-            const SeqB<T> pb = make_seqb<T>(p0, p1);
+        };
+        exps();
+        if (__any(!(ls[0] <= stage_sum_max<T>()))) {
+            float mx = s[0][0];
 #pragma unroll
-            for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Vr, 32 * c, t, lo), pb);
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = (kt == 0 ? 1 : 0); r < 4; ++r) mx = fmax_nn(mx, s[kt][r]);
+            raise_m(mx);
+            exps();
         }
+        l += ls[0];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Vr, 32 * c, t, lo), pb[c]);
     };
-    // One 16-key tile of the short stage, keys x0 .. x0 + 15 of Kr, Vr, those at nv and past masked (k = 16 MFMA).
+    // One 16-key tile of the short stage (the first one taken), keys x0 .. x0 + 15 of Kr, Vr, those at nv and past
+    // masked (k = 16 MFMA). It takes the maximum: m is still -inf at its first tile.
     auto tile16 = [&](const unsigned char* Kr, const unsigned char* Vr, int x0, int nv) {
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
         mma_d_sw<T, DP>(s, Kr, x0, qf, lo);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (x0 + 4 * w.g + r >= nv) s[r] = -INFINITY;
-        track_max(fmax_nn(fmax_nn(s[0], s[1]), fmax_nn(s[2], s[3])));
+        raise_m(fmax_nn(fmax_nn(s[0], s[1]), fmax_nn(s[2], s[3])));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            s[r] = fast_exp2(fmaf(s[r], sc2, -m));
-            l += s[r];
-        }
+        for (int r = 0; r < 4; ++r) s[r] = fast_exp2(fmaf(s[r], sc2, -m));
         const u32x2 pb = pack4<T>(s);
+        l += ET<T>::mma16(u32x2{ones.v[0], ones.v[1]}, pb, f32x4{0.f, 0.f, 0.f, 0.f})[0];
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) acc[t] = ET<T>::mma16(seqa_tr16<T, DP>(Vr, x0, t, lo), pb, acc[t]);
     };
@@ -173,7 +194,6 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         stage(Kr, Kr + C::SB);
     }
     if (!active) return;
-    l = xsum4(l);
     if (own < L) {
         const int64_t r = (int64_t)bh * L + own;
         store_rows<T, DP>(a.out0, r * DP, acc, 1.f / l, DP, w.g);

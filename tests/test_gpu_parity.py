@@ -444,3 +444,26 @@ def test_launcher_input_precision_fp32(cuda):
         outs.append([x.cpu() for x in (o, lse, dq, dk, dv, *hs)])
     for other in outs[1:]:
         assert all(torch.equal(a, b) for a, b in zip(outs[0], other))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rising", [True, False])
+def test_long_forward_moving_maximum(cuda, dtype, rising):
+    """The long forward takes a stage's exponentials against the running reference point and redoes the stage with
+    the row maximum only when a row's sum of them leaves the operand type's safe range (2^32 for bf16, 2^15 for
+    fp16). It takes the short stage (keys 320..332 here) first, then keys 0..319 in 64-key stages. Keys scaled by a
+    ramp in that order make the stage maxima rise ~35 log2 units per stage, past that bound every time (rising), or
+    sit in the first stage taken (falling); every output still matches the oracle."""
+    B, H, L, D = 1, 2, 333, 64
+    _say(f"long forward moving maximum {str(dtype).split('.')[-1]} rising={rising}")
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, torch.float32, seed=7)
+    ramp = torch.linspace(0.0, 1.0, L)
+    ramp[320:] = 0.0  # the short stage, taken first
+    if not rising:
+        ramp = 1.0 - ramp
+    k = k * (1.0 + 59.0 * ramp)[None, None, :, None]  # score spread 1 -> 60
+    q, k, v, do, gq, gk, gv = (t.to(dtype) for t in (q, k, v, do, gq, gk, gv))
+    scale = D**-0.5
+    got = _hip_all(q, k, v, do, gq, gk, gv, scale, cuda)
+    ref = _oracle_all(q, k, v, do, gq, gk, gv, scale, o=got[0], lse=got[1])
+    _compare(got, ref, dtype, f"moving maximum rising={rising}")
