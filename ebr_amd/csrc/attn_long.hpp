@@ -111,10 +111,10 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         for (int e = 0; e < 8; ++e) o[e] = (T)1.f;
         ones.v = __builtin_bit_cast(u32x4, o);
     }
-    // Moves m to the row maximum of scores mx (-inf past L; every stage and tile holds a key below L, so it is finite)
-    // where that exceeds m, rescaling l and acc.
+    // Moves m to the row maximum of scaled scores mx (log2 units, -inf past L; every stage and tile holds a key below
+    // L, so it is finite) where that exceeds m, rescaling l and acc.
     auto raise_m = [&](float mx) {
-        const float mn = fmaxf(m, xmax4(mx) * sc2);
+        const float mn = fmaxf(m, xmax4(mx));
         const float alpha = fast_exp2(m - mn);  // 0 while m = -inf (l and acc are still 0)
         m = mn;
         l *= alpha;
@@ -149,11 +149,11 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         };
         exps();
         if (__any(!(ls[0] <= stage_sum_max<T>()))) {
-            float mx = s[0][0];
+            float mx = s[0][0] * sc2;  // scaled first: the scale may be negative
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                for (int r = (kt == 0 ? 1 : 0); r < 4; ++r) mx = fmax_nn(mx, s[kt][r]);
+                for (int r = (kt == 0 ? 1 : 0); r < 4; ++r) mx = fmax_nn(mx, s[kt][r] * sc2);
             raise_m(mx);
             exps();
         }
@@ -169,11 +169,10 @@ template <typename T, int DP, int NWC> __global__ __launch_bounds__(64 * (NWC + 
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
         mma_d_sw<T, DP>(s, Kr, x0, qf, lo);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (x0 + 4 * w.g + r >= nv) s[r] = -INFINITY;
+        for (int r = 0; r < 4; ++r) s[r] = x0 + 4 * w.g + r < nv ? s[r] * sc2 : -INFINITY;
         raise_m(fmax_nn(fmax_nn(s[0], s[1]), fmax_nn(s[2], s[3])));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s[r] = fast_exp2(fmaf(s[r], sc2, -m));
+        for (int r = 0; r < 4; ++r) s[r] = fast_exp2(s[r] - m);
         const u32x2 pb = pack4<T>(s);
         l += ET<T>::mma16(u32x2{ones.v[0], ones.v[1]}, pb, f32x4{0.f, 0.f, 0.f, 0.f})[0];
 #pragma unroll

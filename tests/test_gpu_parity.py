@@ -467,3 +467,17 @@ def test_long_forward_moving_maximum(cuda, dtype, rising):
     got = _hip_all(q, k, v, do, gq, gk, gv, scale, cuda)
     ref = _oracle_all(q, k, v, do, gq, gk, gv, scale, o=got[0], lse=got[1])
     _compare(got, ref, dtype, f"moving maximum rising={rising}")
+
+
+@pytest.mark.parametrize("scale", [-0.2, 0.0, 0.37])
+@pytest.mark.parametrize("L,dtype", [(81, torch.bfloat16), (200, torch.bfloat16), (900, torch.float16),
+                                     (81, torch.float32), (150, torch.float32)])
+def test_any_scale(cuda, L, dtype, scale):
+    """The scale is any float, as in the reference's ops: negative (the row maximum of the scaled scores is then
+    the scale times the row minimum), zero (uniform P) or large; every kernel family matches the oracle."""
+    B, H, D = 1, 2, 64
+    _say(f"scale={scale} L={L} {str(dtype).split('.')[-1]}")
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, dtype, seed=11)
+    got = _hip_all(q, k, v, do, gq, gk, gv, scale, cuda)
+    ref = _oracle_all(q, k, v, do, gq, gk, gv, scale, o=got[0], lse=got[1])
+    _compare(got, ref, dtype, f"scale={scale} L={L}")
