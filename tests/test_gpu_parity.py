@@ -481,3 +481,35 @@ def test_any_scale(cuda, L, dtype, scale):
     got = _hip_all(q, k, v, do, gq, gk, gv, scale, cuda)
     ref = _oracle_all(q, k, v, do, gq, gk, gv, scale, o=got[0], lse=got[1])
     _compare(got, ref, dtype, f"scale={scale} L={L}")
+
+
+@pytest.mark.parametrize("B,H,L", [(52000, 8, 81), (4700, 8, 900)])
+def test_more_than_2_31_elements(cuda, B, H, L):
+    """Tensors of more than 2^31 elements (B H L D = 2.16e9 at D = 64, 4.3 GB each in bf16): every kernel family
+    (the persistent L = 81 kernels, the long L = 900 kernels) forms its offsets in 64 bits. Inputs are drawn on the
+    GPU; the last slices (offsets past 2^31 elements) and a few random ones are checked against the oracle."""
+    D, dtype = 64, torch.bfloat16
+    assert B * H * L * D > 2**31
+    _say(f"more than 2^31 elements B={B} H={H} L={L}")
+    g = torch.Generator(device=cuda).manual_seed(3)
+    t = [torch.randn((B, H, L, D), generator=g, device=cuda, dtype=torch.float32).to(dtype) for _ in range(7)]
+    for i in range(3):
+        t[i].mul_(0.125)
+    q, k, v, do, gq, gk, gv = t
+    scale = D**-0.5
+    o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
+    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
+    torch.cuda.synchronize()
+    gen = torch.Generator().manual_seed(5)
+    idx = torch.cat([torch.arange(B * H - 4, B * H), torch.randint(0, B * H, (4,), generator=gen)]).to(cuda)
+
+    def pick(x):
+        return x.reshape(B * H, *x.shape[2:])[idx].unsqueeze(0).cpu()
+
+    got = [pick(x) for x in (o, lse, dq, dk, dv, hq, hk, hv, hdo)]
+    sub = [pick(x) for x in t]
+    del t, q, k, v, do, gq, gk, gv, o, lse, dq, dk, dv, hq, hk, hv, hdo
+    torch.cuda.empty_cache()
+    ref = _oracle_all(*sub, scale, o=got[0], lse=got[1])
+    _compare(got, ref, dtype, f"more than 2^31 elements L={L}")
