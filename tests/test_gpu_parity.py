@@ -97,7 +97,7 @@ def test_small_L(cuda, L, dtype):
     _case(2, 3, L, 64, dtype, cuda, seed=L)
 
 
-@pytest.mark.parametrize("L", [129, 200, 333])
+@pytest.mark.parametrize("L", [129, 200, 256, 333])  # 256: no short stage, the first full stage finds m = -inf
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_long_L(cuda, L, dtype):
     _case(2, 2, L, 64, dtype, cuda, seed=L)
