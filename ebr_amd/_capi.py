@@ -18,8 +18,10 @@ DTYPE_F32, DTYPE_BF16, DTYPE_F16, DTYPE_F64 = 0, 1, 2, 3
 OP_FWD, OP_BWD, OP_BWD_BWD = 0, 1, 2
 ERR_HIP_BASE = 1000
 ERR_NOALLOC_SIZE = 6
+ERR_PLAN = 7
+PLAN_AUTO, PLAN_GENERIC, PLAN_RESIDENT, PLAN_PERSISTENT, PLAN_LONG = 0, 1, 2, 3, 4  # EBR_PLAN_*
 NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # EBR_NOALLOC_SCRATCH_BYTES
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I64P = ctypes.POINTER(ctypes.c_int64)
@@ -44,6 +46,30 @@ SIGNATURES = {
         + [_P, _I64P] * 4
         + [_P] * 4
         + [_F32P, _P],
+    ),
+    "ebr_attn_fwd_plan": (
+        ctypes.c_int,
+        [ctypes.c_int] * 5 + [ctypes.c_float] + [_P, _I64P] * 3 + [_P, _F32P, _P, ctypes.c_int],
+    ),
+    "ebr_attn_bwd_plan": (
+        ctypes.c_int,
+        [ctypes.c_int] * 5
+        + [ctypes.c_float]
+        + [_P, _I64P] * 3
+        + [_P, _F32P]
+        + [_P, _I64P]
+        + [_P] * 3
+        + [_F32P, _P, ctypes.c_int],
+    ),
+    "ebr_attn_bwd_bwd_plan": (
+        ctypes.c_int,
+        [ctypes.c_int] * 5
+        + [ctypes.c_float]
+        + [_P, _I64P] * 3
+        + [_P, _F32P]
+        + [_P, _I64P] * 4
+        + [_P] * 4
+        + [_F32P, _P, ctypes.c_int],
     ),
     "ebr_attn_bwd_bwd_noalloc": (
         ctypes.c_int,
@@ -141,7 +167,7 @@ def check(code: int, what: str) -> None:
     msg = f"{what}: {error_string(code)} (code {code})"
     if code == 1:
         raise TypeError(msg)
-    if code == 2:
+    if code in (2, ERR_PLAN):  # a forced plan that does not apply is a bad argument, as an unknown plan key is
         raise ValueError(msg)
     raise RuntimeError(msg)
 

@@ -52,6 +52,7 @@ struct Args {
     float* lse_out;     // (fp64 kernels write it as double)
     float* stats;       // [3][B * H * L] fp32: Dr, E, T (two-launch shapes only)
     int64_t bhl;        // B * H * L
+    int plan;           // EBR_PLAN_*: AUTO (0) for the library's own choice of kernels
 };
 
 template <typename T> __device__ __forceinline__ const T* slice(const Strided& t, int b, int h) {
@@ -786,6 +787,13 @@ static int check_shape(int dtype, int B, int H, int L, int D) {
     return EBR_OK;
 }
 
+// A forced plan must name a family; fp64 has one (its exact kernels) and takes EBR_PLAN_AUTO only.
+static int check_plan(int dtype, int plan) {
+    if (plan < EBR_PLAN_AUTO || plan > EBR_PLAN_LONG) return EBR_ERR_PLAN;
+    if (dtype == EBR_DTYPE_F64 && plan != EBR_PLAN_AUTO) return EBR_ERR_PLAN;
+    return EBR_OK;
+}
+
 // Row starts must be 16-byte aligned, except for fp64 (element-wise kernels): 8-byte aligned elements.
 static int row_align(int es) { return es == 8 ? 8 : 16; }
 
@@ -892,11 +900,14 @@ static void plan_stream(Args& a, int64_t bh, int& grid, int& threads) {
     threads = 64 * STREAM_WAVES;
 }
 
+// Whether a launcher may take kernel family f under the call's plan (EBR_PLAN_AUTO takes the first that applies).
+static bool plan_allows(const Args& a, int f) { return a.plan == EBR_PLAN_AUTO || a.plan == f; }
+
 template <typename T, int DP> struct FwdLaunch {
     static int run(Args a, hipStream_t s) {
         const int64_t bh = (int64_t)a.B * a.H;
         if constexpr (!ET<T>::F32) {
-            if (resident_shape(a, DP, 2, false)) {
+            if (plan_allows(a, EBR_PLAN_RESIDENT) && resident_shape(a, DP, 2, false)) {
                 a.nblk = 1;
                 const dim3 grid((int)bh), block(fused_threads(a.L));
                 switch ((a.L + CH - 1) / CH) {
@@ -909,7 +920,7 @@ template <typename T, int DP> struct FwdLaunch {
             }
         }
         if constexpr (!ET<T>::F32) {
-            if (long_shape(a, DP, false)) {  // streamed stages with a loader wave (k_fwd_long)
+            if (plan_allows(a, EBR_PLAN_LONG) && long_shape(a, DP, false)) {  // streamed stages, a loader wave
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
                     using C = LongCfg<T, DP, NW>;
@@ -921,6 +932,7 @@ template <typename T, int DP> struct FwdLaunch {
                                           : run(std::integral_constant<int, LONG_WAVES>{});
             }
         }
+        if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
         int grid, threads;
         if (fused_shape(a.L)) {
             a.nblk = 1;
@@ -940,7 +952,8 @@ template <typename T, int DP> struct BwdLaunch {
         const int64_t bh = (int64_t)a.B * a.H;
         if constexpr (!ET<T>::F32) {
             a.gq = a.gk = a.gv = a.dO;  // only q, k, v, dO are read
-            if (resident_shape(a, DP, 2, true)) {
+            if ((plan_allows(a, EBR_PLAN_PERSISTENT) || a.plan == EBR_PLAN_RESIDENT) &&
+                resident_shape(a, DP, 2, true)) {
                 a.nblk = 1;
                 const int nch = (a.L + CH - 1) / CH;
                 // persistent, double-buffered with a loader wave (k_bwd_pipe), wherever two buffers of K, V, Q, dO
@@ -954,7 +967,9 @@ template <typename T, int DP> struct BwdLaunch {
                     hipLaunchKernelGGL((k_bwd_pipe<T, DP, N>), pg, dim3(thr), 0, s, a);
                     return launch_rc();
                 };
-                if constexpr (DP <= 64) {
+                if (a.plan == EBR_PLAN_RESIDENT) {
+                    // one (b, h) per workgroup, P and dS recomputed in the col pass (k_bwd_res)
+                } else if constexpr (DP <= 64) {
                     switch (nch) {
                         case 1: return pipe(std::integral_constant<int, 1>{});
                         case 2: return pipe(std::integral_constant<int, 2>{});
@@ -985,6 +1000,7 @@ template <typename T, int DP> struct BwdLaunch {
                     static_assert(16 * BwdPP<T, DP, 4>::NWC == 4 * CH - 16, "HALF at four chunks");
                     if (a.L <= 16 * BwdPP<T, DP, 4>::NWC) return pp(std::integral_constant<int, 4>{}, yes{});
                 }
+                if (a.plan == EBR_PLAN_PERSISTENT) return EBR_ERR_PLAN;  // D = 128, L > 112
                 const dim3 grid((int)bh), block(fused_threads(a.L));
                 switch (nch) {
                     case 1: hipLaunchKernelGGL((k_bwd_res<T, DP, 1>), grid, block, 0, s, a); break;
@@ -996,7 +1012,7 @@ template <typename T, int DP> struct BwdLaunch {
             }
         }
         if constexpr (!ET<T>::F32 && DP <= 64) {
-            if (long_shape(a, DP, true)) {  // streamed stages with a loader wave (k_bwd_long_row, k_bwd_long_col)
+            if (plan_allows(a, EBR_PLAN_LONG) && long_shape(a, DP, true)) {  // k_bwd_long_row, k_bwd_long_col
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
                     using C = LongCfg<T, DP, NW>;
@@ -1012,6 +1028,7 @@ template <typename T, int DP> struct BwdLaunch {
                                           : run(std::integral_constant<int, LONG_WAVES>{});
             }
         }
+        if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
         if (fused_shape(a.L)) {
             a.nblk = 1;
             a.xcd_remap = 0;
@@ -1035,7 +1052,9 @@ template <typename T, int DP> struct BbLaunch {
             a.nblk = 1;
             a.xcd_remap = 0;
             const dim3 grid((int)bh), block(fused_threads(a.L));
-            if (!resident_shape(a, DP, (int)sizeof(T), true)) {
+            if (a.plan == EBR_PLAN_LONG) return EBR_ERR_PLAN;
+            if (a.plan == EBR_PLAN_GENERIC || !resident_shape(a, DP, (int)sizeof(T), true)) {
+                if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
                 hipLaunchKernelGGL((k_bb_fused<T, DP>), grid, block, 0, s, a);
             } else if constexpr (!ET<T>::F32) {
                 const int nch = (a.L + CH - 1) / CH;
@@ -1049,13 +1068,14 @@ template <typename T, int DP> struct BbLaunch {
                     hipLaunchKernelGGL((k_bb_share<T, DP, N>), pg, dim3(thr), 0, s, a);
                     return launch_rc();
                 };
-                if (struct_strides_fit(a)) {
+                if (a.plan != EBR_PLAN_RESIDENT && struct_strides_fit(a)) {
                     if (nch == 1) return share(std::integral_constant<int, 1>{});
                     if (nch == 2) return share(std::integral_constant<int, 2>{});
                     if constexpr (DP <= 64) {
                         if (nch == 3) return share(std::integral_constant<int, 3>{});
                     }
                 }
+                if (a.plan == EBR_PLAN_PERSISTENT) return EBR_ERR_PLAN;  // regions past the LDS, or long strides
                 const bool half = a.L <= nch * CH - 16;  // the last chunk holds one 16-row tile
                 switch (nch) {
                     case 1: hipLaunchKernelGGL((k_bb_res<T, DP, 1, false>), grid, block, 0, s, a); break;
@@ -1073,7 +1093,7 @@ template <typename T, int DP> struct BbLaunch {
             return launch_rc();
         }
         if constexpr (!ET<T>::F32 && DP <= 64) {
-            if (long_shape(a, DP, true)) {  // streamed stages with a loader wave (k_bb_long_row, k_bb_long_col)
+            if (plan_allows(a, EBR_PLAN_LONG) && long_shape(a, DP, true)) {  // k_bb_long_row, k_bb_long_col
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
                     constexpr int NWR = NW == LONG_WAVES_WIDE ? BB_ROW_WAVES_WIDE : NW;
@@ -1096,6 +1116,7 @@ template <typename T, int DP> struct BbLaunch {
                                           : run(std::integral_constant<int, LONG_WAVES>{});
             }
         }
+        if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
         int grid, threads;
         plan_stream(a, bh, grid, threads);
         hipLaunchKernelGGL((k_bb_row<T, DP>), dim3(grid), dim3(threads), 0, s, a);
@@ -1138,6 +1159,7 @@ const char* ebr_attn_error_string(int code) {
             return "row start not 16-byte aligned (8-byte for fp64) (base pointer or a B/H/L stride)";
         case EBR_ERR_NULL: return "required pointer is NULL";
         case EBR_ERR_SCRATCH: return "scratch buffer required for this shape but NULL";
+        case EBR_ERR_PLAN: return "the forced plan (EBR_PLAN_*) does not run this dtype, shape or stride pattern";
         case EBR_ERR_NOALLOC_SIZE:
             return "shape needs more row-statistics scratch than the no-allocation entry point holds "
                    "(EBR_NOALLOC_SCRATCH_BYTES)";
@@ -1160,7 +1182,14 @@ int64_t ebr_attn_scratch_bytes(int op, int B, int H, int L, int D) {  // fp64 ca
 int ebr_attn_fwd(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
                  const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], void* o, void* lse,
                  void* stream) {
+    return ebr_attn_fwd_plan(dtype, B, H, L, D, scale, q, q_str, k, k_str, v, v_str, o, lse, stream, EBR_PLAN_AUTO);
+}
+
+int ebr_attn_fwd_plan(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
+                      const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], void* o,
+                      void* lse, void* stream, int plan) {
     int rc = check_shape(dtype, B, H, L, D);
+    if (!rc) rc = check_plan(dtype, plan);
     if (rc) return rc;
     const int es = elem_size(dtype);
     if ((rc = check_strided(q, q_str, es)) || (rc = check_strided(k, k_str, es)) ||
@@ -1172,6 +1201,7 @@ int ebr_attn_fwd(int dtype, int B, int H, int L, int D, float scale, const void*
     a.v = mk(v, v_str);
     a.out0 = o;
     a.lse_out = static_cast<float*>(lse);
+    a.plan = plan;
     if (dtype == EBR_DTYPE_F64) return f64_fwd(a, (hipStream_t)stream);
     return dispatch<FwdLaunch>(dtype, D, a, (hipStream_t)stream);
 }
@@ -1180,7 +1210,16 @@ int ebr_attn_bwd(int dtype, int B, int H, int L, int D, float scale, const void*
                  const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], const void* o,
                  const void* lse, const void* dO, const int64_t dO_str[3], void* dq, void* dk, void* dv,
                  float* scratch, void* stream) {
+    return ebr_attn_bwd_plan(dtype, B, H, L, D, scale, q, q_str, k, k_str, v, v_str, o, lse, dO, dO_str, dq, dk, dv,
+                             scratch, stream, EBR_PLAN_AUTO);
+}
+
+int ebr_attn_bwd_plan(int dtype, int B, int H, int L, int D, float scale, const void* q, const int64_t q_str[3],
+                      const void* k, const int64_t k_str[3], const void* v, const int64_t v_str[3], const void* o,
+                      const void* lse, const void* dO, const int64_t dO_str[3], void* dq, void* dk, void* dv,
+                      float* scratch, void* stream, int plan) {
     int rc = check_shape(dtype, B, H, L, D);
+    if (!rc) rc = check_plan(dtype, plan);
     if (rc) return rc;
     const int es = elem_size(dtype);
     if ((rc = check_strided(q, q_str, es)) || (rc = check_strided(k, k_str, es)) ||
@@ -1201,6 +1240,7 @@ int ebr_attn_bwd(int dtype, int B, int H, int L, int D, float scale, const void*
     a.out1 = dk;
     a.out2 = dv;
     a.stats = scratch;
+    a.plan = plan;
     if (dtype == EBR_DTYPE_F64) return f64_bwd(a, (hipStream_t)stream);
     return dispatch<BwdLaunch>(dtype, D, a, (hipStream_t)stream);
 }
@@ -1211,7 +1251,18 @@ int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale, const v
                      const int64_t gq_str[3], const void* gk, const int64_t gk_str[3], const void* gv,
                      const int64_t gv_str[3], void* hq, void* hk, void* hv, void* hdo, float* scratch,
                      void* stream) {
+    return ebr_attn_bwd_bwd_plan(dtype, B, H, L, D, scale, q, q_str, k, k_str, v, v_str, o, lse, dO, dO_str, gq,
+                                 gq_str, gk, gk_str, gv, gv_str, hq, hk, hv, hdo, scratch, stream, EBR_PLAN_AUTO);
+}
+
+int ebr_attn_bwd_bwd_plan(int dtype, int B, int H, int L, int D, float scale, const void* q,
+                          const int64_t q_str[3], const void* k, const int64_t k_str[3], const void* v,
+                          const int64_t v_str[3], const void* o, const void* lse, const void* dO,
+                          const int64_t dO_str[3], const void* gq, const int64_t gq_str[3], const void* gk,
+                          const int64_t gk_str[3], const void* gv, const int64_t gv_str[3], void* hq, void* hk,
+                          void* hv, void* hdo, float* scratch, void* stream, int plan) {
     int rc = check_shape(dtype, B, H, L, D);
+    if (!rc) rc = check_plan(dtype, plan);
     if (rc) return rc;
     const int es = elem_size(dtype);
     if ((rc = check_strided(q, q_str, es)) || (rc = check_strided(k, k_str, es)) ||
@@ -1238,6 +1289,7 @@ int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale, const v
     a.out2 = hv;
     a.out3 = hdo;
     a.stats = scratch;
+    a.plan = plan;
     if (dtype == EBR_DTYPE_F64) return f64_bwd_bwd(a, (hipStream_t)stream);
     return dispatch<BbLaunch>(dtype, D, a, (hipStream_t)stream);
 }

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define EBR_ATTN_ABI_VERSION 2
+#define EBR_ATTN_ABI_VERSION 3
 
 enum {
     EBR_DTYPE_F32 = 0,
@@ -48,6 +48,7 @@ enum {
     EBR_ERR_NULL = 4,        /* a required pointer is NULL */
     EBR_ERR_SCRATCH = 5,     /* scratch is NULL but this shape needs one (see ebr_attn_scratch_bytes) */
     EBR_ERR_NOALLOC_SIZE = 6, /* the shape needs more scratch than EBR_NOALLOC_SCRATCH_BYTES (no-allocation entry) */
+    EBR_ERR_PLAN = 7,        /* the forced plan does not run this dtype, shape or stride pattern (*_plan entries) */
     EBR_ERR_HIP_BASE = 1000, /* EBR_ERR_HIP_BASE + hipError_t of a failed launch */
 };
 
@@ -93,6 +94,44 @@ int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale,
                      const void* gk, const int64_t gk_str[3],
                      const void* gv, const int64_t gv_str[3],
                      void* hq, void* hk, void* hv, void* hdo, float* scratch, void* stream);
+
+/* Kernel families the *_plan entry points can force: the reference's launch-plan override (PLAN_OVERRIDE, a module
+ * dictionary read by the Triton launchers, models/fused_attn/triton_kernels.py:610-615, 673-676) as a per-call
+ * argument, since the library keeps no state. EBR_PLAN_AUTO is the library's own choice, the one the entry points
+ * without a plan argument always make. A family that does not run the call's dtype, shape or strides returns
+ * EBR_ERR_PLAN before anything is enqueued; fp64 takes EBR_PLAN_AUTO only. */
+enum {
+    EBR_PLAN_AUTO = 0,
+    EBR_PLAN_GENERIC = 1,    /* any of fp32, bf16, fp16: one (b, h) per workgroup up to L = 128, two launches above */
+    EBR_PLAN_RESIDENT = 2,   /* bf16 / fp16, L <= 128, D of 32, 64 or 128: one (b, h) per workgroup, operands in LDS */
+    EBR_PLAN_PERSISTENT = 3, /* bf16 / fp16, L <= 128 (bwd, bwd_bwd): persistent workgroups with loader waves */
+    EBR_PLAN_LONG = 4,       /* bf16 / fp16, L > 128: 64-row stages streamed by a loader wave (D 32, 64; fwd 128) */
+};
+
+/* ebr_attn_fwd, ebr_attn_bwd and ebr_attn_bwd_bwd with the kernel family forced by plan (EBR_PLAN_*); same
+ * arguments otherwise. The reference sets its plans through PLAN_OVERRIDE (triton_kernels.py:612-615, 673-676). */
+int ebr_attn_fwd_plan(int dtype, int B, int H, int L, int D, float scale,
+                      const void* q, const int64_t q_str[3],
+                      const void* k, const int64_t k_str[3],
+                      const void* v, const int64_t v_str[3],
+                      void* o, void* lse, void* stream, int plan);
+int ebr_attn_bwd_plan(int dtype, int B, int H, int L, int D, float scale,
+                      const void* q, const int64_t q_str[3],
+                      const void* k, const int64_t k_str[3],
+                      const void* v, const int64_t v_str[3],
+                      const void* o, const void* lse,
+                      const void* dO, const int64_t dO_str[3],
+                      void* dq, void* dk, void* dv, float* scratch, void* stream, int plan);
+int ebr_attn_bwd_bwd_plan(int dtype, int B, int H, int L, int D, float scale,
+                          const void* q, const int64_t q_str[3],
+                          const void* k, const int64_t k_str[3],
+                          const void* v, const int64_t v_str[3],
+                          const void* o, const void* lse,
+                          const void* dO, const int64_t dO_str[3],
+                          const void* gq, const int64_t gq_str[3],
+                          const void* gk, const int64_t gk_str[3],
+                          const void* gv, const int64_t gv_str[3],
+                          void* hq, void* hk, void* hv, void* hdo, float* scratch, void* stream, int plan);
 
 /* Bytes of the library's own device scratch array behind ebr_attn_bwd_bwd_noalloc (one copy per GPU). */
 #define EBR_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)

@@ -179,6 +179,24 @@ def test_launcher_argument_errors():
             kernels.attn_bwd_bwd(q, q, q, q, q[..., 0], q, None, None, None, None, 0.5, input_precision=prec)
 
 
+def test_plan_override_keys_and_values(monkeypatch):
+    """PLAN_OVERRIDE takes the reference's plan keys for the forward and the two backward modes and this library's
+    kernel families as values; anything else raises ValueError before any other check or launch."""
+    from ebr_amd.fused_attn import kernels
+
+    q = torch.zeros(1, 2, 3, 8)
+    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {"bob_row": (16, 16, 4, 1)})
+    with pytest.raises(ValueError, match="not tunable"):
+        kernels.attn_fwd(q, q, q, 0.5)
+    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {"bwd_mode": "atomic"})
+    with pytest.raises(ValueError, match="names no kernel family"):
+        kernels.attn_bwd(q, q, q, q, q[..., 0], q, 0.5)
+    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {"fwd": "long", "bwd_mode": "resident", "bob_mode": "auto"})
+    assert (kernels._plan("fwd"), kernels._plan("bwd_mode"), kernels._plan("bob_mode")) == (4, 2, 0)
+    with pytest.raises(ValueError, match="GPU tensors"):  # a valid dictionary reaches the usual checks
+        kernels.attn_fwd(q, q, q, 0.5)
+
+
 def test_rows_keeps_aligned_views_and_copies_others():
     x = torch.zeros(2, 5, 3, 4, 64, dtype=torch.bfloat16)  # [B, L, 3, H, D] projection
     q = x[:, :, 0].transpose(1, 2)

@@ -40,9 +40,9 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_arch_and_error_texts():
     lib = _capi.load()
-    assert lib.ebr_attn_abi_version() == _capi.ABI_VERSION == 2
+    assert lib.ebr_attn_abi_version() == _capi.ABI_VERSION == 3
     assert lib.ebr_attn_arch() == b"gfx950"
-    for code in (0, 1, 2, 3, 4, 5, 6):
+    for code in (0, 1, 2, 3, 4, 5, 6, 7):
         assert lib.ebr_attn_error_string(code)
     assert b"no-allocation" in lib.ebr_attn_error_string(_capi.ERR_NOALLOC_SIZE)
     assert b"unknown" in lib.ebr_attn_error_string(77)
@@ -124,6 +124,8 @@ def test_check_maps_codes_to_reference_exceptions():
         _capi.check(2, "x")
     with pytest.raises(RuntimeError):
         _capi.check(3, "x")
+    with pytest.raises(ValueError, match="plan"):
+        _capi.check(_capi.ERR_PLAN, "x")
     with pytest.raises(RuntimeError, match="hip|error|invalid"):
         _capi.check(_capi.ERR_HIP_BASE + 1, "x")
     _capi.check(0, "x")
@@ -150,3 +152,14 @@ def test_noalloc_entry_rejects_shapes_beyond_its_array_before_any_hip_call():
     assert lib.ebr_attn_bwd_bwd_noalloc(_capi.DTYPE_BF16, 0, H, L, D, ctypes.c_float(0.125), *tail) == 2  # B < 1
     assert lib.ebr_attn_bwd_bwd_noalloc(_capi.DTYPE_BF16, 2, 2, 81, 64, ctypes.c_float(0.125), *tail[:-5],
                                         None, 16, 16, 16, None) == 4  # hq NULL: L <= 128 needs no scratch lookup
+
+
+def test_plan_entries_reject_unknown_plans_and_fp64_plans_before_any_hip_call():
+    """The *_plan entry points check the plan (a family code, EBR_PLAN_AUTO only for fp64) with the other arguments,
+    before anything is enqueued; placeholder pointers never reach a kernel."""
+    lib = _capi.load()
+    s = (ctypes.c_int64 * 3)(64 * 8, 64 * 8, 64)
+    p = ctypes.c_void_p(16)  # aligned, never dereferenced
+    for dtype, plan in ((_capi.DTYPE_BF16, 9), (_capi.DTYPE_BF16, -1), (_capi.DTYPE_F64, _capi.PLAN_GENERIC)):
+        rc = lib.ebr_attn_fwd_plan(dtype, 1, 1, 8, 64, ctypes.c_float(0.125), p, s, p, s, p, s, p, p, None, plan)
+        assert rc == _capi.ERR_PLAN, (dtype, plan, rc)

@@ -513,3 +513,58 @@ def test_more_than_2_31_elements(cuda, B, H, L):
     torch.cuda.empty_cache()
     ref = _oracle_all(*sub, scale, o=got[0], lse=got[1])
     _compare(got, ref, dtype, f"more than 2^31 elements L={L}")
+
+
+# Forced kernel families (kernels.PLAN_OVERRIDE over the C ABI's *_plan entry points): every family on shapes it
+# runs, each checked against the oracle; a family that does not run the shape raises ValueError.
+PLAN_CASES = [
+    # (B, H, L, D, dtype, {op key: (families that run, families that raise)})
+    (2, 3, 81, 64, torch.bfloat16, {"fwd": ("generic resident", "persistent long"),
+                                    "bwd_mode": ("generic resident persistent", "long"),
+                                    "bob_mode": ("generic resident persistent", "long")}),
+    (2, 2, 100, 64, torch.bfloat16, {"bwd_mode": ("generic resident persistent", "long"),
+                                     "bob_mode": ("generic resident", "persistent long")}),
+    (2, 2, 100, 128, torch.float16, {"fwd": ("generic resident", "long"),
+                                     "bwd_mode": ("generic resident persistent", "long"),
+                                     "bob_mode": ("generic resident", "persistent")}),
+    (2, 2, 200, 64, torch.bfloat16, {"fwd": ("generic long", "resident persistent"),
+                                     "bwd_mode": ("generic long", "resident persistent"),
+                                     "bob_mode": ("generic long", "resident persistent")}),
+    (2, 2, 200, 128, torch.bfloat16, {"fwd": ("generic long", "resident"), "bwd_mode": ("generic", "long"),
+                                      "bob_mode": ("generic", "long")}),
+    (2, 2, 81, 64, torch.float32, {"fwd": ("generic", "resident long"), "bwd_mode": ("generic", "persistent"),
+                                   "bob_mode": ("generic", "resident persistent long")}),
+]
+
+
+@pytest.mark.parametrize("case", range(len(PLAN_CASES)))
+def test_forced_plans(cuda, case, monkeypatch):
+    from ebr_amd.fused_attn import kernels
+
+    B, H, L, D, dtype, plans = PLAN_CASES[case]
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, dtype, seed=case)
+    scale = D**-0.5
+    t = [x.to(cuda) for x in (q, k, v, do, gq, gk, gv)]
+    ref = None
+    for key, (run, refuse) in plans.items():
+        for fam in run.split():
+            label = f"plan {key}={fam} B={B} H={H} L={L} D={D} {str(dtype).split('.')[-1]}"
+            _say(label)
+            monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {key: fam})
+            o, lse = kernels.attn_fwd(*t[:3], scale)
+            dq, dk, dv = kernels.attn_bwd(*t[:3], o, lse, t[3], scale)
+            hs = kernels.attn_bwd_bwd(*t[:3], o, lse, t[3], dq, *t[4:], scale)
+            torch.cuda.synchronize()
+            got = [x.cpu() for x in (o, lse, dq, dk, dv, *hs)]
+            ref = _oracle_all(q, k, v, do, gq, gk, gv, scale, o=got[0], lse=got[1])
+            _compare(got, ref, dtype, label)
+        for fam in refuse.split():
+            monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {key: fam})
+            o, lse = kernels.attn_fwd(*t[:3], scale) if key != "fwd" else (None, None)
+            with pytest.raises(ValueError, match="plan"):
+                if key == "fwd":
+                    kernels.attn_fwd(*t[:3], scale)
+                elif key == "bwd_mode":
+                    kernels.attn_bwd(*t[:3], o, lse, t[3], scale)
+                else:
+                    kernels.attn_bwd_bwd(*t[:3], o, lse, t[3], None, *t[4:], scale)
