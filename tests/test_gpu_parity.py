@@ -568,3 +568,23 @@ def test_forced_plans(cuda, case, monkeypatch):
                     kernels.attn_bwd(*t[:3], o, lse, t[3], scale)
                 else:
                     kernels.attn_bwd_bwd(*t[:3], o, lse, t[3], None, *t[4:], scale)
+
+
+def _random_cases(n, seed=2024):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for i in range(n):
+        dtype = [torch.float32, torch.bfloat16, torch.float16][int(torch.randint(0, 3, (1,), generator=g))]
+        L = int(torch.randint(1, 320, (1,), generator=g))
+        D = int(torch.randint(1, 129, (1,), generator=g))
+        B = int(torch.randint(1, 4, (1,), generator=g))
+        H = int(torch.randint(1, 4, (1,), generator=g))
+        out.append((i, B, H, L, D, dtype))
+    return out
+
+
+@pytest.mark.parametrize("i,B,H,L,D,dtype", _random_cases(40))
+def test_random_shapes(cuda, i, B, H, L, D, dtype):
+    """Seeded random shapes (any L up to 319, any head dim up to 128, three dtypes, small B and H): whatever plan
+    and padding the ops pick, every output matches the oracle."""
+    _case(B, H, L, D, dtype, cuda, seed=100 + i)
