@@ -181,12 +181,16 @@ def test_config2_maze_bf16_full_size(cuda):
         (48, 8, 517, 64, torch.float16),
         (64, 8, 177, 64, torch.bfloat16),
         (64, 8, 161, 128, torch.bfloat16),
+        (48, 8, 240, 64, torch.bfloat16),
+        (64, 8, 340, 128, torch.float16),
+        (16, 8, 1024, 64, torch.bfloat16),
     ],
 )
 def test_long_wide_grids_ragged_L(cuda, B, H, L, D, dtype):
     """Grids large enough for the wide long-sequence workgroups (7 compute waves; 10 in the bwd_bwd row kernel, with
     its own 160-row blocking), L not a multiple of any block or stage (last stages of 1 to 4 live 16-row tiles); 8
-    random slices checked."""
+    random slices checked. At L = 240, 340 and 1024 the last 112-row block holds one live 16-row strip (after a
+    short stage of 48, 20 or no rows)."""
     _sampled(B, H, L, D, dtype, cuda, 8, seed=L)
 
 
