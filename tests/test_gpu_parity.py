@@ -233,6 +233,36 @@ def test_strided_views(cuda, B, L, D):
     _compare(got, ref, torch.bfloat16, f"strided B={B} L={L} D={D}")
 
 
+@pytest.mark.parametrize("B,H,L,D", [(32, 4, 900, 64), (96, 4, 333, 128)])
+def test_strided_views_long_wide_grids(cuda, B, H, L, D):
+    """Every input a non-contiguous view at the long-sequence shapes with the wide (7-wave) workgroups: q, k, v
+    slices of one [B, L, 3, H, D] projection, dO and the cotangents transposed [B, L, H, D] tensors; 6 random
+    slices checked against the oracle on contiguous copies."""
+    _say(f"strided long views B={B} H={H} L={L} D={D}")
+    g = torch.Generator().manual_seed(L)
+    qkv = (torch.randn(B, L, 3, H, D, generator=g) * 0.125).to(torch.bfloat16)
+    rest = [torch.randn(B, L, H, D, generator=g).to(torch.bfloat16) for _ in range(4)]
+    qkv_d = qkv.to(cuda)
+    q, k, v = (qkv_d[:, :, i].transpose(1, 2) for i in range(3))
+    do, gq, gk, gv = (t.to(cuda).transpose(1, 2) for t in rest)
+    assert not (q.is_contiguous() or do.is_contiguous() or gk.is_contiguous())
+    scale = D**-0.5
+    o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, do, scale)
+    hq, hk, hv, hdo = torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, do, dq, gq, gk, gv, scale)
+    torch.cuda.synchronize()
+    idx = torch.randperm(B * H, generator=g)[:6]
+
+    def pick(t):
+        return t.reshape(B * H, *t.shape[2:])[idx].unsqueeze(0)
+
+    got = [pick(x.cpu()) for x in (o, lse, dq, dk, dv, hq, hk, hv, hdo)]
+    ins = [qkv[:, :, i].transpose(1, 2).contiguous() for i in range(3)] + [t.transpose(1, 2).contiguous() for t in rest]
+    qs, ks, vs, dos, gqs, gks, gvs = (pick(t) for t in ins)
+    ref = _oracle_all(qs, ks, vs, dos, gqs, gks, gvs, scale, o=got[0], lse=got[1])
+    _compare(got, ref, torch.bfloat16, f"strided long B={B} H={H} L={L} D={D}")
+
+
 def test_wide_row_stride(cuda):
     """Views whose row stride exceeds 16 KiB (a [B, L, 3, H, D] projection with H = 48): the persistent backward of
     the backward cannot hold that stride in a structured buffer descriptor and takes the one-slice kernel."""
