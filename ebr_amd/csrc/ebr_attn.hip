@@ -871,7 +871,12 @@ static bool long_wide(int64_t bh, int L) {
     const int64_t rows = 16 * LONG_WAVES_WIDE;
     return bh * ((L + rows - 1) / rows) >= 1024;
 }
-constexpr int BB_ROW_STAGE = 64;  // k_bb_long_row's stage depth (32 rows with three workgroups per CU was slower)
+// k_bb_long_row's stage depth: 128 rows for the wide workgroup, the one workgroup a CU holds at its register use
+// (two 64 KB stage buffers; half the barriers and stage hand-overs of 64-row stages: Maze bwd_bwd 1.016 -> 1.001 ms,
+// measured), 64 for the 4-wave workgroups of small grids, two of which share a CU's LDS (32 rows with three
+// workgroups per CU was slower).
+constexpr int BB_ROW_STAGE = 64;
+constexpr int BB_ROW_STAGE_WIDE = 128;
 // k_bb_long_row needs about 150 VGPRs, so a SIMD holds 3 of its waves and a CU one 8-wave workgroup: 10 compute waves
 // (+ the loader) fill the CU with one workgroup of 160 rows instead (Maze bwd_bwd 1.26 -> 1.18 ms, measured). The
 // other long kernels keep 7: their wider variants measured slower (bwd with 9: 0.51 -> 0.70 ms; fwd with 6 or 13).
@@ -1097,11 +1102,12 @@ template <typename T, int DP> struct BbLaunch {
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
                     constexpr int NWR = NW == LONG_WAVES_WIDE ? BB_ROW_WAVES_WIDE : NW;
+                    constexpr int STG = NW == LONG_WAVES_WIDE ? BB_ROW_STAGE_WIDE : BB_ROW_STAGE;
                     {  // the row kernel has a row blocking of its own; the col kernel reads only its statistics
                         Args ar = a;
                         using CR = LongCfg<T, DP, NWR>;
                         plan_long(ar, bh, CR::ROWS);
-                        hipLaunchKernelGGL((k_bb_long_row<T, DP, NWR, BB_ROW_STAGE>), dim3((int)(bh * ar.nblk)),
+                        hipLaunchKernelGGL((k_bb_long_row<T, DP, NWR, STG>), dim3((int)(bh * ar.nblk)),
                                            dim3(CR::THREADS), 0, s, ar);
                     }
                     const int rc = launch_rc();
