@@ -200,11 +200,10 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     using LY = Lay<T, DP>;
     constexpr int Lp = NCH * CH;
     constexpr int RB = Lp * Sw<DP>::ROWB;
-    // K, V | a row-store area per wave, unless it would leave room for fewer than two workgroups per CU (D = 128,
-    // L > 96: the stores then go out directly)
-    constexpr int STG = 2 * NCH * RowStage16<T, DP>::BYTES;
-    constexpr bool STAGED = 2 * (2 * RB + STG) <= 160 * 1024;
-    __shared__ __align__(1024) unsigned char smem[2 * RB + (STAGED ? STG : 0)];
+    // K, V. Once every wave has its scores, the K region holds the waves' row-store areas (the active waves' 16 rows
+    // each, at most Lp rows), so the stores cost no LDS of their own.
+    static_assert(2 * NCH * RowStage16<T, DP>::BYTES <= RB, "row-store areas in the K region");
+    __shared__ __align__(1024) unsigned char smem[2 * RB];
     const WaveIds w = wave_ids();
     const int nw = w.nthr >> 6;
     const int bh = blockIdx.x;
@@ -244,6 +243,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         }
     });
     const float m = xmax4(mx);
+    lds_barrier();  // every active wave done with K (inactive ones have left)
     float lsum = 0.f;
     f32x4 acc[LY::NT];
 #pragma unroll
@@ -262,12 +262,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         for (int t = 0; t < LY::NT; ++t) acc[t] = mma_seq<T>(acc[t], seqa_tr<T, DP>(Vr, C * CH, t, lo), pb);
     });
     lsum = xsum4(lsum);
-    if constexpr (STAGED) {
-        store_acc_staged<T, DP>(a.out0, ((int64_t)bh * L + row0) * DP, L - row0, acc, 1.f / lsum,
-                                smem + 2 * RB + w.wave * RowStage16<T, DP>::BYTES, w.lane);
-    } else if (own < L) {
-        store_rows<T, DP>(a.out0, ((int64_t)bh * L + own) * DP, acc, 1.f / lsum, DP, w.g);
-    }
+    store_acc_staged<T, DP>(a.out0, ((int64_t)bh * L + row0) * DP, L - row0, acc, 1.f / lsum,
+                            Kr + w.wave * RowStage16<T, DP>::BYTES, w.lane);
     if (own < L && w.g == 0) a.lse_out[(int64_t)bh * L + own] = m * (1.f / LOG2E) + logf(lsum);
 }
 
