@@ -295,8 +295,9 @@ def bb_kernel_name(cfg: dict) -> str:
     if L > 128:
         if dt != torch.float32 and D in (32, 64):
             wide = cfg["B"] * cfg["H"] * -(-L // 112) >= 1024  # long_wide() in ebr_attn.hip
-            nw, nwr = (7, 10) if wide else (4, 4)  # LONG_WAVES_WIDE, BB_ROW_WAVES_WIDE
-            return f"k_bb_long_row<{DT_NAME[dt]}, {D}, {nwr}, 64> + k_bb_long_col<{DT_NAME[dt]}, {D}, {nw}>"
+            # LONG_WAVES_WIDE, BB_ROW_WAVES_WIDE, BB_ROW_STAGE_WIDE; LONG_WAVES, BB_ROW_STAGE
+            nw, nwr, stg = (7, 10, 128) if wide else (4, 4, 64)
+            return f"k_bb_long_row<{DT_NAME[dt]}, {D}, {nwr}, {stg}> + k_bb_long_col<{DT_NAME[dt]}, {D}, {nw}>"
         return f"k_bb_row<{DT_NAME[dt]}, {D}> + k_bb_col<{DT_NAME[dt]}, {D}>"
     if dt != torch.float32 and D in (32, 64, 128):
         nch = (L + 31) // 32
