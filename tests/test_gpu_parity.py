@@ -194,6 +194,14 @@ def test_long_wide_grids_ragged_L(cuda, B, H, L, D, dtype):
     _sampled(B, H, L, D, dtype, cuda, 8, seed=L)
 
 
+@pytest.mark.parametrize("B,H,L", [(1, 2, 2500), (8, 8, 2500)])
+def test_long_sequences_many_stages(cuda, B, H, L):
+    """L = 2500 (40 stages of 64 rows, the last 4 rows short; 23 row blocks of 112, or 16 of the bwd_bwd row kernel's
+    160 rows, none of them a multiple): the small-grid (4 waves) and wide (7 and 10 waves) long-sequence workgroups;
+    2 random slices checked."""
+    _sampled(B, H, L, 64, torch.bfloat16, cuda, 2, seed=L)
+
+
 def test_config4_shape_bf16(cuda):
     """Config 4's attention shape (L=100) on a reduced batch; all slices checked."""
     _case(40, 8, 100, 64, torch.bfloat16, cuda, seed=4)
