@@ -163,3 +163,23 @@ def test_plan_entries_reject_unknown_plans_and_fp64_plans_before_any_hip_call():
     for dtype, plan in ((_capi.DTYPE_BF16, 9), (_capi.DTYPE_BF16, -1), (_capi.DTYPE_F64, _capi.PLAN_GENERIC)):
         rc = lib.ebr_attn_fwd_plan(dtype, 1, 1, 8, 64, ctypes.c_float(0.125), p, s, p, s, p, s, p, p, None, plan)
         assert rc == _capi.ERR_PLAN, (dtype, plan, rc)
+
+
+def test_integration_guide_stubs_compile_and_call_declared_entry_points():
+    """The ctypes stubs the integration guide shows maintainers compile, and call only entry points the headers
+    declare (their GPU test runs them against the oracle)."""
+    import ast
+
+    text = (ROOT / "INTEGRATION.md").read_text()
+    stubs = [b for b in re.findall(r"```python\n(.*?)```", text, re.S) if "ctypes stub over libebr_attn.so" in b]
+    assert len(stubs) == 3
+    declared = set(_declared())
+    for src in stubs:
+        tree = ast.parse(src)
+        called = {
+            n.func.attr
+            for n in ast.walk(tree)
+            if isinstance(n, ast.Call) and isinstance(n.func, ast.Attribute)
+            and isinstance(n.func.value, ast.Name) and n.func.value.id == "_lib"
+        }
+        assert called and called <= declared, called - declared
