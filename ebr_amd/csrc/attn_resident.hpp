@@ -451,9 +451,18 @@ template <typename T, int DP, int NCH> struct BwdPipe {
     static constexpr bool FITS = SMEM <= 160 * 1024;
 };
 
+// Byte offset of keys key0 .. key0 + 3 (key0 a multiple of 4) of tile row ``row``. The 8-byte group of four keys
+// moves to group (key0 / 4) ^ 2 in rows with bit 3 set: under the pitch (an odd multiple of 32 bytes past a multiple
+// of 256) rows r and r + 8 start on the same bank, so a store's half-wave of 16 rows at two groups each hit every bank
+// twice; with the swap it hits each once (bwd_bwd at config 1: 162.6 -> 158.2 us). The transposed reads take 8 rows
+// and 4 groups per half-wave, conflict-free either way.
+__device__ __forceinline__ int tile_off(int row, int pitch, int key0) {
+    return row * pitch + ((((key0 >> 2) ^ ((row >> 2) & 2))) << 3);
+}
+
 // 8-byte tile write: row ``row`` (query), keys key0 .. key0 + 3 (4 packed 16-bit values).
 __device__ __forceinline__ void tile_store8(unsigned char* tile, int pitch, int row, int key0, u32x2 v) {
-    *reinterpret_cast<u32x2*>(tile + row * pitch + key0 * 2) = v;
+    *reinterpret_cast<u32x2*>(tile + tile_off(row, pitch, key0)) = v;
 }
 
 // B operand of a col pass from a [query][key] tile: lane (key = kb + l16, group g), k-slot 4 h + k holds
@@ -461,7 +470,7 @@ __device__ __forceinline__ void tile_store8(unsigned char* tile, int pitch, int 
 template <typename T>
 __device__ __forceinline__ SeqB<T> tile_seqb(const unsigned char* tile, int pitch, int x0, int kb, int l16, int g) {
     const int k = l16 >> 2, j = l16 & 3;
-    const unsigned char* p = tile + (x0 + 4 * g + k) * pitch + (kb + 4 * j) * 2;
+    const unsigned char* p = tile + tile_off(x0 + 4 * g + k, pitch, kb + 4 * j);  // row + 16 below: same swap
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)p);
     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EBR_LDS s16x4*)(p + 16 * pitch));
     const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
