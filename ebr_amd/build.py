@@ -59,6 +59,13 @@ def compile_flags(arch: str = ARCH) -> list:
     ]
 
 
+def link_flags(arch: str = ARCH, extra_flags: tuple = ()) -> list:
+    """Flags of the link step: the target, and every extra flag except those that only steer preprocessing (-I, -D,
+    -U), so that flags that matter at link time too (-fgpu-rdc, -g, host-side instrumentation) reach it."""
+    pre = ("-I", "-D", "-U")
+    return [f"--offload-arch={arch}", "-shared", "-fPIC", *(f for f in extra_flags if not f.startswith(pre))]
+
+
 def _run(cmd: list, verbose: bool) -> str:
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -69,22 +76,23 @@ def _run(cmd: list, verbose: bool) -> str:
     return proc.stderr
 
 
-def build(verbose: bool = False, extra_flags: tuple = (), jobs: int = 0) -> Path:
-    """Compile every HIP source (in parallel, one object each) and link the in-tree shared library; return its path."""
+def build(verbose: bool = False, extra_flags: tuple = (), jobs: int = 0, arch: str = ARCH) -> Path:
+    """Compile every HIP source (in parallel, one object each) and link the in-tree shared library; return its path.
+    ``extra_flags`` go to every compile and, bar preprocessor flags, to the link."""
     OUT_DIR.mkdir(parents=True, exist_ok=True)
     out = OUT_DIR / LIB_NAME
     tmp = out.with_suffix(".so.tmp")
     obj_dir = OUT_DIR / "obj"
     obj_dir.mkdir(exist_ok=True)
     cc = hipcc()
-    flags = [*compile_flags(), *extra_flags]
+    flags = [*compile_flags(arch), *extra_flags]
     objs = [obj_dir / (src.stem + ".o") for src in SOURCES]
     t0 = time.time()
     workers = jobs or min(len(SOURCES), max(1, os.cpu_count() or 1))
     with ThreadPoolExecutor(max_workers=workers) as pool:
         logs = list(pool.map(lambda so: _run([cc, *flags, "-c", str(so[0]), "-o", str(so[1])], verbose),
                              zip(SOURCES, objs)))
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
+    _run([cc, *link_flags(arch, tuple(extra_flags)), *map(str, objs), "-o", str(tmp)], verbose)
     if verbose:
         noise = "is not a recognized feature for this target"
         for log in logs:

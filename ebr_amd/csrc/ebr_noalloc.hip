@@ -6,7 +6,10 @@
 // The array is a file-scope __device__ variable: every GPU the library runs on holds its own copy, at its own address,
 // until the process ends. Host code never passes the array's name to a kernel (on the host that name is a stand-in,
 // not a device address); it passes the address hipGetSymbolAddress returns for the current device, looked up once per
-// device on the entry point's first call there. Every call on one GPU shares that GPU's copy and leaves the last
+// device on the entry point's first call there. That first call may come inside HIP stream capture (a caller
+// recording a graph): the lookup enqueues nothing, and it runs with this thread's capture mode switched to relaxed,
+// so a capture in global or thread-local mode neither rejects it nor is invalidated by it. The per-device address
+// table is the library's only mutable host state. Every call on one GPU shares that GPU's copy and leaves the last
 // call's contents in it: calls that overlap on one GPU (two streams, two threads) race. Nothing has to start at zero:
 // the row kernel writes every statistic the column kernel reads.
 #include <hip/hip_runtime.h>
@@ -35,7 +38,12 @@ int device_scratch(float** out) {
     float* p = scratch_of[dev].load(std::memory_order_acquire);
     if (!p) {
         void* addr = nullptr;
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        e = hipThreadExchangeStreamCaptureMode(&mode);  // relaxed for the lookup; the caller's mode comes back below
+        if (e != hipSuccess) return EBR_ERR_HIP_BASE + (int)e;
         e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+        const hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e == hipSuccess && e2 != hipSuccess) e = e2;
         if (e != hipSuccess || !addr) return EBR_ERR_HIP_BASE + (int)(e != hipSuccess ? e : hipErrorInvalidSymbol);
         p = static_cast<float*>(addr);
         scratch_of[dev].store(p, std::memory_order_release);  // every thread that races here stores the same value

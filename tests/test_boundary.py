@@ -180,19 +180,38 @@ def test_launcher_argument_errors():
 
 
 def test_plan_override_keys_and_values(monkeypatch):
-    """PLAN_OVERRIDE takes the reference's plan keys for the forward and the two backward modes and this library's
-    kernel families as values; anything else raises ValueError before any other check or launch."""
+    """PLAN_OVERRIDE takes the reference's keys and values (triton_kernels.py:610-615): block-shape tuples are
+    accepted and select nothing, the modes 'single' and 'two' map onto this library's one-launch and streamed
+    families, 'atomic' raises; this library's family names work on the three selecting keys. Anything else raises
+    ValueError before any other check or launch."""
+    from ebr_amd import _capi
     from ebr_amd.fused_attn import kernels
 
     q = torch.zeros(1, 2, 3, 8)
-    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {"bob_row": (16, 16, 4, 1)})
-    with pytest.raises(ValueError, match="not tunable"):
+    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {"bob_tile": (16, 16, 4, 1)})
+    with pytest.raises(ValueError, match="not a plan key"):
         kernels.attn_fwd(q, q, q, 0.5)
+    for bad in ({"bob_row": (16, 16, 4)}, {"bwd_col": "long"}, {"fwd": "two"}, {"bob_mode": (64, 32, 4, 3)},
+                {"bwd_dq": (16, 16, 4, 0)}, {"bwd_mode": "fast"}):
+        monkeypatch.setattr(kernels, "PLAN_OVERRIDE", bad)
+        with pytest.raises(ValueError, match="names no kernel family"):
+            kernels.attn_bwd(q, q, q, q, q[..., 0], q, 0.5)
     monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {"bwd_mode": "atomic"})
-    with pytest.raises(ValueError, match="names no kernel family"):
+    with pytest.raises(ValueError, match="atomic"):
         kernels.attn_bwd(q, q, q, q, q[..., 0], q, 0.5)
     monkeypatch.setattr(kernels, "PLAN_OVERRIDE", {"fwd": "long", "bwd_mode": "resident", "bob_mode": "auto"})
     assert (kernels._plan("fwd"), kernels._plan("bwd_mode"), kernels._plan("bob_mode")) == (4, 2, 0)
+    # the reference's own default plans for bf16 at N = 81 (triton_kernels.py:641-652) and at N = 900
+    ref81 = dict(fwd=(64, 32, 4, 3), bwd_mode="single", bwd_single=(32, 128, 4, 1), bwd_col=(64, 64, 4, 3),
+                 bwd_dq=(64, 32, 4, 3), bob_mode="single", bob_single=(16, 128, 4, 1), bob_row=(64, 32, 4, 3),
+                 bob_col=(64, 64, 4, 2))
+    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", ref81)
+    assert [kernels._plan(k, 81) for k in ("fwd", "bwd_mode", "bob_mode")] == [_capi.PLAN_AUTO] * 3
+    with pytest.raises(ValueError, match="one-launch"):
+        kernels._plan("bob_mode", 900)
+    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", dict(ref81, fwd=(64, 64, 4, 3), bwd_mode="two", bob_mode="two"))
+    assert [kernels._plan(k, 900) for k in ("fwd", "bwd_mode", "bob_mode")] == [_capi.PLAN_AUTO] * 3
+    assert [kernels._plan(k, 81) for k in ("bwd_mode", "bob_mode")] == [_capi.PLAN_GENERIC] * 2
     with pytest.raises(ValueError, match="GPU tensors"):  # a valid dictionary reaches the usual checks
         kernels.attn_fwd(q, q, q, 0.5)
 

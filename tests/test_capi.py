@@ -140,6 +140,32 @@ def test_build_recipe_targets_gfx950_without_packed_fp32():
     assert flags[i - 1] == "-Xclang" and flags[i - 2] == "-target-feature"
 
 
+def test_build_forwards_extra_flags_to_compile_and_link(monkeypatch, tmp_path):
+    """build() passes its extra flags to every compile and (bar -I / -D / -U) to the link, with one target arch."""
+    from ebr_amd import build
+
+    cmds = []
+
+    def fake_run(cmd, verbose):
+        cmds.append(cmd)
+        Path(cmd[-1]).write_bytes(b"")
+        return ""
+
+    monkeypatch.setattr(build, "_run", fake_run)
+    monkeypatch.setattr(build, "hipcc", lambda: "hipcc")
+    monkeypatch.setattr(build, "OUT_DIR", tmp_path)
+    extra = ("-fgpu-rdc", "-DEBR_PROBE=1", "-g", "-I/tmp/x")
+    out = build.build(extra_flags=extra, jobs=1, arch="gfx950")
+    assert out == tmp_path / build.LIB_NAME
+    compiles = [c for c in cmds if "-c" in c]
+    (link,) = [c for c in cmds if "-shared" in c]
+    assert len(compiles) == len(build.SOURCES)
+    for c in compiles:
+        assert all(f in c for f in extra) and "--offload-arch=gfx950" in c
+    assert "-fgpu-rdc" in link and "-g" in link and "--offload-arch=gfx950" in link
+    assert not any(f.startswith(("-D", "-I")) for f in link)
+
+
 def test_noalloc_entry_rejects_shapes_beyond_its_array_before_any_hip_call():
     """ebr_attn_bwd_bwd_noalloc checks the row-statistics size against EBR_NOALLOC_SCRATCH_BYTES first (no GPU needed:
     nothing is looked up or enqueued), and otherwise validates arguments exactly as ebr_attn_bwd_bwd does."""

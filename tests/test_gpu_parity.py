@@ -612,6 +612,38 @@ def test_forced_plans(cuda, case, monkeypatch):
                     kernels.attn_bwd_bwd(*t[:3], o, lse, t[3], None, *t[4:], scale)
 
 
+REF_PLAN_CASES = [
+    # (B, H, L, D, dtype, PLAN_OVERRIDE written against the reference's launchers)
+    (2, 3, 81, 64, torch.bfloat16, {"fwd": (64, 32, 4, 3), "bwd_mode": "single", "bwd_single": (32, 128, 4, 1),
+                                    "bob_mode": "single", "bob_single": (16, 128, 4, 1)}),
+    (2, 3, 81, 64, torch.bfloat16, {"bwd_mode": "two", "bob_mode": "two", "bwd_col": (64, 64, 4, 3),
+                                    "bob_row": (64, 32, 4, 3), "bob_col": (64, 64, 4, 2)}),
+    (2, 2, 200, 64, torch.bfloat16, {"fwd": (64, 64, 4, 3), "bwd_mode": "two", "bob_mode": "two"}),
+    (2, 2, 81, 64, torch.float32, {"fwd": (128, 32, 8, 3), "bwd_mode": "two", "bob_mode": "single"}),
+]
+
+
+@pytest.mark.parametrize("case", range(len(REF_PLAN_CASES)))
+def test_reference_plan_override_values(cuda, case, monkeypatch):
+    """PLAN_OVERRIDE dictionaries in the reference's own form (block-shape tuples, 'single' / 'two' modes) run the
+    launchers to the oracle's values."""
+    from ebr_amd.fused_attn import kernels
+
+    B, H, L, D, dtype, override = REF_PLAN_CASES[case]
+    _say(f"reference-style plan override {override} B={B} H={H} L={L} D={D} {str(dtype).split('.')[-1]}")
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, dtype, seed=40 + case)
+    scale = D**-0.5
+    t = [x.to(cuda) for x in (q, k, v, do, gq, gk, gv)]
+    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", override)
+    o, lse = kernels.attn_fwd(*t[:3], scale)
+    dq, dk, dv = kernels.attn_bwd(*t[:3], o, lse, t[3], scale)
+    hs = kernels.attn_bwd_bwd(*t[:3], o, lse, t[3], dq, *t[4:], scale)
+    torch.cuda.synchronize()
+    got = [x.cpu() for x in (o, lse, dq, dk, dv, *hs)]
+    ref = _oracle_all(q, k, v, do, gq, gk, gv, scale, o=got[0], lse=got[1])
+    _compare(got, ref, dtype, f"reference-style plan override case {case}")
+
+
 def _random_cases(n, seed=2024):
     g = torch.Generator().manual_seed(seed)
     out = []

@@ -161,3 +161,26 @@ def test_raw_ops_check_operands(cuda):
         torch.ops.ebr_fused.rope_merge(dq, dq[:, :1], dq, cos, cos, none)
     with pytest.raises(ValueError):
         torch.ops.ebr_fused.rope_merge(dq, dq, dq, cos[:, :8], cos[:, :8], none)
+
+
+def test_fp64_on_the_gpu_runs_the_dense_functions_to_second_order(cuda):
+    """fp64 GPU tensors (gradcheck) go to the dense functions, which the reference's kernel check does too
+    (rope_split.py:18-19): values equal the oracle's, and gradcheck / gradgradcheck pass on the device."""
+    _say("rope fp64 on the GPU: dense path, gradcheck and gradgradcheck")
+    qkv, (gq, gk, gv) = oracle.make_rope_inputs(1, 6, 2, 8, dtype=torch.float64, seed=6)
+    cos, sin = (t.double() for t in _tables(8, 6))
+    got = rs.rope_split(qkv.to(cuda), cos.to(cuda), sin.to(cuda), 2)
+    want = oracle.ref_split(qkv, cos, sin, 2)
+    assert all(torch.allclose(a.cpu(), b, rtol=0, atol=1e-15) for a, b in zip(got, want))
+    m = torch.ops.ebr_fused.rope_merge(gq.to(cuda), gk.to(cuda), gv.to(cuda), cos.to(cuda), sin.to(cuda),
+                                       torch.zeros(0, device=cuda))
+    assert torch.allclose(m.cpu(), oracle.ref_merge(gq, gk, gv, cos, sin), rtol=0, atol=1e-15)
+    x = qkv.to(cuda).requires_grad_(True)
+    c, s = cos.to(cuda), sin.to(cuda)
+
+    def f(x):
+        q, k, v = rs.rope_split(x, c, s, 2)
+        return (q * k).sum(-1) + v.pow(2).sum(-1)
+
+    assert torch.autograd.gradcheck(f, (x,))
+    assert torch.autograd.gradgradcheck(f, (x,))
