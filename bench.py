@@ -516,14 +516,15 @@ def _median_ms(fn, n: int) -> float:
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
 
 
-def ebr_train(steps: int, warmup: int, cpu_batches=(8, 16, 48), cpu_full: bool = True):
+def ebr_train(steps: int, warmup: int, cpu_batches=(8, 16, 48), cpu_full: int = 3):
     """BASELINE config 3: 2 post-norm blocks, hidden 512, 8 x 64 heads, SwiGLU x4, mean-pooled linear energy head;
     x ~ U{0..10} [384, 81]; z ~ N(0, 1) [384, 81, 512]; 16 steps z <- z - 0.1 dE/dz with create_graph; CE of a linear
     decode head to random targets; backward; bf16. GPU: the fused (gfx950) attention, median of ``steps`` timed steps,
     eager and graph-captured. CPU: the same step eager with the 'math' attention on the host's cores at the batch
     sizes ``cpu_batches`` (median of 3 each after one warm-up), a least-squares line t = a + b * batch through them,
-    and, with ``cpu_full``, one whole step at batch 384. The speed-up is taken against the whole step when it was
-    timed, else against the line at batch 384 (the step has a fixed cost: t is not proportional to the batch)."""
+    and the median of ``cpu_full`` whole steps at batch 384 (BASELINE's "median of 3 full steps"). The speed-up is
+    taken against the whole steps when they were timed, else against the line at batch 384 (the step has a fixed
+    cost: t is not proportional to the batch)."""
     from ebr_amd import energy as en
 
     B, L, V = 384, 81, 11
@@ -595,26 +596,31 @@ def ebr_train(steps: int, warmup: int, cpu_batches=(8, 16, 48), cpu_full: bool =
         slope = sum((b - mb) * (per_batch[b] - mt) for b in bs) / sum((b - mb) ** 2 for b in bs)
         icpt = mt - slope * mb
         fit_sec = icpt + slope * B
-        full_sec = None
+        full_sec, full_all = None, []
         if cpu_full:
-            # one whole step at the GPU's batch (its warm-up is the batch-48 step above: same code, same shapes but B)
-            cm.zero_grad(set_to_none=True)
-            cd.zero_grad(set_to_none=True)
-            t = time.perf_counter()
-            en.train_step(cm, cd, x.cpu(), z0.cpu(), tg.cpu())
-            full_sec = time.perf_counter() - t
+            # whole steps at the GPU's batch (their warm-up is the batch-48 step above: same code, same shapes but B)
+            cx, cz, ct = x.cpu(), z0.cpu(), tg.cpu()
+            for _ in range(cpu_full):
+                cm.zero_grad(set_to_none=True)
+                cd.zero_grad(set_to_none=True)
+                t = time.perf_counter()
+                en.train_step(cm, cd, cx, cz, ct)
+                full_all.append(time.perf_counter() - t)
+            full_sec = statistics.median(full_all)
         sec = full_sec if full_sec is not None else fit_sec
         out["cpu"] = {"steps_per_s": round(1.0 / sec, 5), "cores": cores, "kind": "port",
                       "seconds_at_batch": {str(b): round(t, 3) for b, t in per_batch.items()},
                       "fit_seconds": {"fixed": round(icpt, 4), "per_row": round(slope, 5),
                                       f"at_batch_{B}": round(fit_sec, 3)},
                       "seconds_full_step": None if full_sec is None else round(full_sec, 3),
+                      "seconds_full_steps_all": [round(t, 3) for t in full_all],
                       "peak_host_rss_gb": round(resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 2**20, 1),
-                      "basis": "one whole batch-384 step" if full_sec is not None else "the fitted line at batch 384",
+                      "basis": f"median of {len(full_all)} whole batch-{B} steps" if full_sec is not None else
+                      f"the fitted line at batch {B}",
                       "sample": f"the same step eager with the math attention at batches {bs} (median of 3 after 1 "
                       f"warm-up each) and a least-squares line a + b * batch through them"
-                      + (f"; one whole step at batch {B}, timed once, is the basis" if full_sec is not None else
-                         f"; the line at batch {B} is the basis"), "cpu": cpu_info()}
+                      + (f"; the median of {len(full_all)} whole steps at batch {B} is the basis" if full_sec is not None
+                         else f"; the line at batch {B} is the basis"), "cpu": cpu_info()}
         out["speedup_vs_cpu"] = round(out["steps_per_s"] / out["cpu"]["steps_per_s"], 1)
         out["graph_speedup_vs_cpu"] = round(graphed["steps_per_s"] / out["cpu"]["steps_per_s"], 1)
         out["speedup_vs_cpu_fit"] = round(fit_sec * out["steps_per_s"], 1)
@@ -984,7 +990,7 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-cpu-full-step", action="store_true",
-                    help="config 3's host baseline from the fitted line alone (no whole batch-384 step on the host)")
+                    help="config 3's host baseline from the fitted line alone (no whole batch-384 steps on the host)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -1100,7 +1106,7 @@ def main() -> int:
     if not args.no_ebr:
         log("EBR training step (config 3)")
         out["ebr_train"] = ebr_train(args.ebr_steps, 2, () if args.no_cpu else (8, 16, 48),
-                                     cpu_full=not args.no_cpu_full_step)
+                                     cpu_full=0 if args.no_cpu_full_step else 3)
         log(f"EBR train: {out['ebr_train']}")
     if not args.no_ebr_infer:
         log("EBR inference descent (config 4)")

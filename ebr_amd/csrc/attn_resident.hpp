@@ -1185,19 +1185,29 @@ template <typename T, int DP, int NCH, bool HALF> __global__ __launch_bounds__(5
 // are 3 GEMM units: 12 for the whole backward of the backward, the minimum. One compute wave per 16 rows covers every
 // tile row (padded rows are written as 0).
 //
-// Persistent, with loader waves: the workgroup (one per CU: the regions fill its LDS) takes slices s, s + G, s + 2 G,
-// ... (G = gridDim.x). Besides the compute waves it has NWL loader waves, which hold the whole next slice in their
-// registers while the compute waves work on the current one, and write it into each region as soon as a barrier
-// frees it. They also reduce rowsum(dO o O) and scale lse, so the compute waves issue no global loads at all. The
-// loads go through registers (structured buffer loads) because an LDS transpose read right after an outstanding
-// global -> LDS load makes the compiler wait for that load. Per slice s with next slice n = s + G:
-//   compute waves                           loader waves
-//   row pass (s)                            load every input row of n into registers
+// Persistent: the workgroup (one per CU: the regions fill its LDS) takes slices s, s + G, s + 2 G, ... (G =
+// gridDim.x). The compute waves issue no global stores: a store instruction stalls its wave while the memory system
+// is busy (all CUs store and load at once), and those stalls sat on the slice's critical path (at config 1 the kernel
+// ran 35 us faster with its output stores left out). They hand their rounded output rows to the NWL loader waves
+// through LDS instead, in the natural swizzled row layout of the regions: hQ, hdO into the K, gK regions right after
+// barrier A (the row pass no longer reads them), hK, hV into the tile area right after barrier B (the col pass no
+// longer reads it), each hand-off published by an LDS counter that every compute wave bumps once per slice. The
+// loader waves read the rows into registers and store them to HBM as whole rows; they also hold the next slice's K,
+// gK, V, gV in registers and write them into their regions once the hQ, hdO rows there are read. Each compute wave
+// fetches its own 16 rows of the next slice's Q, gQ, dO, O and their lse into registers at the end of its row pass,
+// writes its Q, gQ, dO rows into their regions once the col pass is done with them, and takes its row pass operands,
+// rowsum(dO o O) and lse straight from those registers, so no wave waits for another's row statistics. Global loads
+// go through registers (structured buffer loads in the loaders) because an LDS transpose read right after an
+// outstanding global -> LDS load makes the compiler wait for that load. Per slice s with next slice n = s + G:
+//   compute waves                                   loader waves
+//   row pass (s); fetch own rows (n)                load K, gK, V, gV of n into registers; store hK, hV of s - G
 //   --- barrier A: tiles complete, K, gK, V, gV (s) no longer read
-//   store hQ, hdO (s); col pass (s)         write K, gK, V, gV (n); rowsum(dO o O) (n) into registers
-//   --- barrier B: tiles and Q, gQ, dO (s) no longer read
-//   store hK, hV (s)                        write Q, gQ, dO (n), rowsum(dO o O) (n), lse (n)
-//   --- barrier C: every region holds n
+//   hQ, hdO rows (s) -> K, gK regions; count        wait for the count; read them; write K, gK, V, gV (n);
+//   col pass (s)                                    store hQ, hdO (s)
+//   --- barrier B: tiles and Q, gQ, dO (s) no longer read; K, gK, V, gV (n) in place
+//   hK, hV rows (s) -> tile area; count             wait for the count; read them; count
+//   own rows of Q, gQ, dO (n) -> regions; row pass (n), its first tile write after the loaders' count
+// Every counter wait is bounded (SPIN_MAX polls), so no wave can wait forever.
 // =====================================================================================================================
 
 template <typename T, int DP, int NCH> struct BbShare {
@@ -1207,16 +1217,18 @@ template <typename T, int DP, int NCH> struct BbShare {
     static constexpr int TB = LP * TP;            // one tile
     static constexpr int NWC = 2 * NCH;           // compute waves (16 rows each)
     static constexpr int NB = LP / Sw<DP>::RPI;   // 1 KB blocks per tensor
-    // loader waves: each holds NB / NWL of the 1 KB blocks of each of the 8 staged tensors in registers (32 NB / NWL
-    // VGPRs); two, or four where two would need more than 192 VGPRs each (only D = 128 with two chunks)
-    static constexpr int NWL = 32 * NB / 2 > 192 ? 4 : 2;
+    // loader waves: each holds NB / NWL of the 1 KB blocks of each of K, gK, V, gV (16 NB / NWL VGPRs) and of two
+    // output tensors (8 NB / NWL VGPRs) in registers
+    static constexpr int NWL = 24 * NB / 2 > 192 ? 4 : 2;
     static_assert(NWC + NWL <= 8, "launch bound of 512 threads");
     static constexpr int NPER = NB / NWL;         // blocks per loader wave and tensor
     static_assert(NPER * NWL == NB, "the loader waves split every tensor's 1 KB blocks evenly");
-    static_assert(NWL * 64 >= LP, "one loader lane per row for lse");
-    static constexpr int STG = 3 * TB + 7 * RB + 2 * LP * 4;  // byte offset of the compute waves' store areas
-    // K, gK, V, gV | Q, gQ, dO | dS2, dS, Pa | rowsum(dO o O), lse * log2 e | a row-store area per compute wave
-    static constexpr int SMEM = STG + NWC * RowStage16<T, DP>::BYTES;
+    static constexpr int TILES = 7 * RB;          // byte offset of the tile area: dS2, dS, Pa
+    // the tile area also parks hK and hV (two natural regions) between barrier B and the loaders' reads
+    static constexpr int PARK = 3 * TB > 2 * RB ? 3 * TB : 2 * RB;
+    static constexpr int CNT = TILES + PARK;      // three LDS counters
+    // K, gK, V, gV | Q, gQ, dO | dS2, dS, Pa (hK, hV parked) | counters
+    static constexpr int SMEM = CNT + 16;
     static constexpr int THREADS = 64 * (NWC + NWL);
 };
 
@@ -1242,7 +1254,8 @@ template <int DP, int NPER> struct StageLanes {
 };
 
 // Register staging of one tensor's share. fetch() issues the loads (row index clamped to L - 1, so every access is
-// inside the slice); put() writes them to a swizzled region, rows past L as 0.
+// inside the slice); put() writes them to a swizzled region, rows past L as 0. take() reads a region's rows back and
+// store() writes them to a contiguous [L, DP] output slice, whole rows, rows past L skipped.
 template <typename T, int DP, int NPER> struct RowStage {
     u32x4 v[NPER];
     __device__ __forceinline__ void fetch(const T* slice, int64_t srow, int L, const StageLanes<DP, NPER>& sl) {
@@ -1258,17 +1271,43 @@ template <typename T, int DP, int NPER> struct RowStage {
         for (int i = 0; i < NPER; ++i)
             *reinterpret_cast<u32x4*>(region + (wave + i * nw) * 1024 + 16 * lane) = sl.x[i] < L ? v[i] : z;
     }
+    __device__ __forceinline__ void take(const unsigned char* region, int wave, int nw, int lane) {
+#pragma unroll
+        for (int i = 0; i < NPER; ++i)
+            v[i] = *reinterpret_cast<const u32x4*>(region + (wave + i * nw) * 1024 + 16 * lane);
+    }
+    __device__ __forceinline__ void store(void* out, int64_t slice_off, int L, const StageLanes<DP, NPER>& sl) const {
+        T* o = reinterpret_cast<T*>(out) + slice_off;
+#pragma unroll
+        for (int i = 0; i < NPER; ++i)
+            if (sl.x[i] < L) *reinterpret_cast<u32x4*>(o + (int64_t)sl.x[i] * DP + sl.coff[i] / 2) = v[i];
+    }
 };
 
+// LDS counters of the output hand-offs (monotonic; each compute or loader wave adds 1 per slice).
+constexpr int SPIN_MAX = 1 << 20;  // polls before a wait gives up (never reached when every wave runs)
 
-// The loader waves' registers: every input row of one slice.
+__device__ __forceinline__ void count_up(unsigned int* c, int lane) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this wave's LDS writes before the count
+    if (lane == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void wait_count(unsigned int* c, unsigned int target) {
+    for (int i = 0; i < SPIN_MAX; ++i) {
+        const unsigned int v =
+            __builtin_amdgcn_readfirstlane(__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (v >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // the counted writes before this wave's reads
+}
+
+// The loader waves' registers: the K, gK, V, gV rows of one slice, and two output tensors' rows in transit.
 template <typename T, int DP, int NCH> struct BbLoader {
     using R = BbShare<T, DP, NCH>;
     using RS = RowStage<T, DP, R::NPER>;
     StageLanes<DP, R::NPER> sl;
-    RS k, gk, v, gv, q, gq, dO, o;
-    float lse;
-    float dr[R::NPER];  // rowsum(dO o O) of the rows this lane's chunks belong to (prep_rest)
+    RS k, gk, v, gv, o0, o1;
     int lw, lane;
     __device__ __forceinline__ BbLoader(int lw_, int lane_) : sl(lw_, R::NWL, lane_), lw(lw_), lane(lane_) {}
     __device__ __forceinline__ void fetch(const Args& a, int s) {
@@ -1278,12 +1317,6 @@ template <typename T, int DP, int NCH> struct BbLoader {
         gk.fetch(slice<T>(a.gk, b, h), a.gk.sl, L, sl);
         v.fetch(slice<T>(a.v, b, h), a.v.sl, L, sl);
         gv.fetch(slice<T>(a.gv, b, h), a.gv.sl, L, sl);
-        q.fetch(slice<T>(a.q, b, h), a.q.sl, L, sl);
-        gq.fetch(slice<T>(a.gq, b, h), a.gq.sl, L, sl);
-        dO.fetch(slice<T>(a.dO, b, h), a.dO.sl, L, sl);
-        o.fetch(reinterpret_cast<const T*>(a.o) + (int64_t)s * L * DP, DP, L, sl);
-        const int t = lw * 64 + lane;
-        lse = a.lse[(int64_t)s * L + (t < L ? t : L - 1)];  // unconditional load
     }
     __device__ __forceinline__ void put_k4(unsigned char* smem, int L) const {
         k.put(smem, L, sl, lw, R::NWL, lane);
@@ -1291,32 +1324,77 @@ template <typename T, int DP, int NCH> struct BbLoader {
         v.put(smem + 2 * R::RB, L, sl, lw, R::NWL, lane);
         gv.put(smem + 3 * R::RB, L, sl, lw, R::NWL, lane);
     }
-    // rowsum(dO o O) of the fetched rows, in registers: the row's NCK lanes hold its chunks of both. Runs while the
-    // compute waves are still in the col pass, so that put_rest after its barrier only writes LDS.
-    __device__ __forceinline__ void prep_rest() {
-        constexpr int NCK = Sw<DP>::NCK;
-#pragma unroll
-        for (int i = 0; i < R::NPER; ++i) {
-            float d = dot8<T>(dO.v[i], o.v[i]);
-#pragma unroll
-            for (int m = 1; m < NCK; m <<= 1) d += __shfl_xor(d, m);
-            dr[i] = d;
-        }
+    // two parked output tensors (rows in the region layout, R::RB bytes each, back to back) into registers
+    __device__ __forceinline__ void take(const unsigned char* park) {
+        o0.take(park, lw, R::NWL, lane);
+        o1.take(park + R::RB, lw, R::NWL, lane);
     }
-    __device__ __forceinline__ void put_rest(unsigned char* smem, float* drl, float* lse2, int L) const {
-        q.put(smem + 4 * R::RB, L, sl, lw, R::NWL, lane);
-        gq.put(smem + 5 * R::RB, L, sl, lw, R::NWL, lane);
-        dO.put(smem + 6 * R::RB, L, sl, lw, R::NWL, lane);
-        constexpr int NCK = Sw<DP>::NCK;
-#pragma unroll
-        for (int i = 0; i < R::NPER; ++i) {
-            const int x = sl.x[i];
-            if (lane % NCK == 0) drl[x] = x < L ? dr[i] : 0.f;
-        }
-        const int t = lw * 64 + lane;
-        if (t < R::LP) lse2[t] = t < L ? lse * LOG2E : INFINITY;  // padded query rows: P = 0
+    __device__ __forceinline__ void store(void* out0, void* out1, int s, int L) const {
+        const int64_t off = (int64_t)s * L * DP;
+        o0.store(out0, off, L, sl);
+        o1.store(out1, off, L, sl);
     }
 };
+
+// A compute wave's own rows of one slice: Q, gQ, dO and O in the own-fragment layout (lane (row l16, group g) holds
+// d = c * CW + g * VEC ..), and the row's lse. fetch() loads them raw from row min(own, L - 1), so every access is
+// inside the slice and no select waits on a load; clear() zeroes the rows past L where they are consumed.
+template <typename T, int DP> struct OwnRows {
+    OwnFrag<T, DP> q, gq, dO, o;
+    float lse;
+    static __device__ __forceinline__ void raw(OwnFrag<T, DP>& f, const T* base, int64_t srow, int r, int g) {
+        using LY = Lay<T, DP>;
+        const T* p = base + (int64_t)r * srow + g * LY::VEC;
+#pragma unroll
+        for (int c = 0; c < LY::NC; ++c) f.v[c] = *reinterpret_cast<const u32x4*>(p + c * LY::CW);
+    }
+    __device__ __forceinline__ void fetch(const Args& a, int s, int own, int g) {
+        const int L = a.L;
+        const int b = s / a.H, h = s - b * a.H;
+        const int r = own < L ? own : L - 1;
+        raw(q, slice<T>(a.q, b, h), a.q.sl, r, g);
+        raw(gq, slice<T>(a.gq, b, h), a.gq.sl, r, g);
+        raw(dO, slice<T>(a.dO, b, h), a.dO.sl, r, g);
+        raw(o, reinterpret_cast<const T*>(a.o) + (int64_t)s * L * DP, DP, r, g);
+        lse = a.lse[(int64_t)s * L + r];
+    }
+    __device__ __forceinline__ void clear(bool live) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int c = 0; c < Lay<T, DP>::NC; ++c) {
+            q.v[c] = live ? q.v[c] : z;
+            gq.v[c] = live ? gq.v[c] : z;
+            dO.v[c] = live ? dO.v[c] : z;
+            o.v[c] = live ? o.v[c] : z;
+        }
+        lse = live ? lse : INFINITY;  // padded query rows: P = 0
+    }
+    // rows row0 .. row0 + 15 of the Q, gQ, dO regions
+    __device__ __forceinline__ void put(unsigned char* Qr, unsigned char* gQr, unsigned char* Or, int row0,
+                                        const LaneOff<T, DP>& lo) const {
+        const int base = row0 * Sw<DP>::ROWB;
+#pragma unroll
+        for (int c = 0; c < Lay<T, DP>::NC; ++c) {
+            *reinterpret_cast<u32x4*>(Qr + base + lo.a[c]) = q.v[c];
+            *reinterpret_cast<u32x4*>(gQr + base + lo.a[c]) = gq.v[c];
+            *reinterpret_cast<u32x4*>(Or + base + lo.a[c]) = dO.v[c];
+        }
+    }
+};
+
+// A seq-contraction accumulator's 16 rows (lane (row l16, group g) holds columns 16 t + 4 g .. + 3), scaled by mul
+// and rounded, into rows row0 .. row0 + 15 of a region in the swizzled natural layout.
+template <typename T, int DP>
+__device__ __forceinline__ void park_rows(unsigned char* region, int row0, const f32x4 (&acc)[DP / 16], float mul,
+                                          int l16, int g) {
+    using S = Sw<DP>;
+    unsigned char* p = region + (row0 + l16) * S::ROWB + 8 * (g & 1);
+#pragma unroll
+    for (int t = 0; t < DP / 16; ++t) {
+        const int c = 2 * t + (g >> 1);  // 16-byte chunk of columns 16 t + 4 g
+        *reinterpret_cast<u32x2*>(p + 16 * (c ^ S::swz(l16))) = pack4<T>(acc[t] * mul);
+    }
+}
 
 template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_bb_share(Args a) {
     using LY = Lay<T, DP>;
@@ -1331,37 +1409,43 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     unsigned char* gVr = smem + 3 * R::RB;
     unsigned char* Qr = smem + 4 * R::RB;
     unsigned char* gQr = smem + 5 * R::RB;
-    unsigned char* Or = smem + 6 * R::RB;  // dO
-    unsigned char* T2 = smem + 7 * R::RB;  // dS2
-    unsigned char* T1 = T2 + R::TB;        // dS
-    unsigned char* Ta = T2 + 2 * R::TB;    // Pa
-    float* drl = reinterpret_cast<float*>(T2 + 3 * R::TB);
-    float* lsel = drl + R::LP;
+    unsigned char* Or = smem + 6 * R::RB;    // dO
+    unsigned char* T2 = smem + R::TILES;     // dS2
+    unsigned char* T1 = T2 + R::TB;          // dS
+    unsigned char* Ta = T2 + 2 * R::TB;      // Pa
+    unsigned char* park = T2;                // hK, hV between barrier B and the loaders' reads
+    unsigned int* cnt = reinterpret_cast<unsigned int*>(smem + R::CNT);  // hQ/hdO parked, hK/hV parked, hK/hV read
     int s = blockIdx.x;
+    if (w.tid < 3) cnt[w.tid] = 0u;  // before the first barrier
 
     if (w.wave >= R::NWC) {
         // ---- loader waves
         BbLoader<T, DP, NCH> ld(w.wave - R::NWC, w.lane);
         ld.fetch(a, s);
         ld.put_k4(smem, L);
-        ld.prep_rest();
-        ld.put_rest(smem, drl, lsel, L);
         lds_barrier();
+        unsigned int it = 0;
+        int prev = -1;  // slice whose hK, hV rows sit in the registers, not yet stored
         while (true) {
             const int n = s + (int)gridDim.x;
             const bool more = n < nbh;  // uniform over the workgroup
             if (more) ld.fetch(a, n);
+            if (prev >= 0) ld.store(a.out1, a.out2, prev, L);
             lds_barrier();  // A
-            if (more) {
-                ld.put_k4(smem, L);
-                ld.prep_rest();
-            }
+            wait_count(cnt, R::NWC * (it + 1));
+            ld.take(Kr);  // hQ, hdO of s from the K, gK regions
+            if (more) ld.put_k4(smem, L);
+            ld.store(a.out0, a.out3, s, L);
             lds_barrier();  // B
+            wait_count(cnt + 1, R::NWC * (it + 1));
+            ld.take(park);  // hK, hV of s
+            count_up(cnt + 2, w.lane);
+            prev = s;
             if (!more) break;
-            ld.put_rest(smem, drl, lsel, L);
-            lds_barrier();  // C
             s = n;
+            ++it;
         }
+        ld.store(a.out1, a.out2, prev, L);
         return;
     }
 
@@ -1371,15 +1455,14 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
     const int row0 = w.wave * 16;
     const int own = row0 + w.l16;
     const bool active = row0 < L;
+    const bool live = own < L;
     const LaneOff<T, DP> lo(w.l16, w.g);
-    unsigned char* stage = smem + R::STG + w.wave * RowStage16<T, DP>::BYTES;
-    // hK, hV of the previous slice, rounded and packed, stored once this slice's row pass is done: right after the
-    // col pass every workgroup on the chip stores at once while the loaders' fetch of the next slice is in flight,
-    // and the store issue stalls the compute waves.
-    u32x2 pend_k[LY::NT], pend_v[LY::NT];
-    int64_t pend_r = 0;
-    bool pend = false;
+    OwnRows<T, DP> nx;  // this wave's rows of the slice the next row pass takes
+    nx.fetch(a, s, own, w.g);
+    nx.clear(live);
+    nx.put(Qr, gQr, Or, row0, lo);
     lds_barrier();  // the first slice is in LDS
+    unsigned int it = 0;
     while (true) {
         const int n = s + (int)gridDim.x;
         const bool more = n < nbh;
@@ -1390,12 +1473,9 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
 #pragma unroll
         for (int t = 0; t < LY::NT; ++t) hq[t] = hdo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (active) {
-            OwnFrag<T, DP> qf, gqf, df;
-            own_from_lds<T, DP>(qf, Qr, row0, lo);  // rows past L are 0 in the regions
-            own_from_lds<T, DP>(gqf, gQr, row0, lo);
-            own_from_lds<T, DP>(df, Or, row0, lo);
-            const float lse2 = lsel[own];
-            const float dr = drl[own];
+            const OwnFrag<T, DP> qf = nx.q, gqf = nx.gq, df = nx.dO;  // rows past L are 0
+            const float lse2 = nx.lse * LOG2E;                       // +inf past L
+            const float dr = xsum4(frag_dot<T, DP>(nx.dO, nx.o));     // rowsum(dO o O)
             float pf[NCH][8], dsf[NCH][8], paf[NCH][8], m1f[NCH][8];
             float e_acc = 0.f, t_acc = 0.f;
             static_for<0, NCH>([&](auto cc) {
@@ -1432,6 +1512,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             });
             const float E = xsum4(e_acc);
             const float Tm = xsum4(t_acc);
+            wait_count(cnt + 2, R::NWL * it);  // the loaders have read the previous slice's hK, hV from the tiles
             static_for<0, NCH>([&](auto cc) {
                 constexpr int C = decltype(cc)::value;
                 const int x0 = C * CH;
@@ -1461,19 +1542,18 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 }
             });
         } else {
+            wait_count(cnt + 2, R::NWL * it);
             zero_tile_rows<NCH>(T2, T1, Ta, R::TP, own, w.g);
         }
-        if (pend) {  // wave-uniform
-            store_rows_staged<T, DP>(a.out1, pend_r, L - row0, pend_k, stage, w.lane);
-            store_rows_staged<T, DP>(a.out2, pend_r, L - row0, pend_v, stage, w.lane);
-            pend = false;
-        }
+        // this wave's rows of the next slice (or this one again after the last: the load stays unconditional); they
+        // have the col pass and two barriers to land
+        nx.fetch(a, more ? n : s, own, w.g);
         lds_barrier();  // A
         if (active) {
-            const int64_t r = ((int64_t)s * L + row0) * DP;
-            store_acc_staged<T, DP>(a.out0, r, L - row0, hq, sc, stage, w.lane);
-            store_acc_staged<T, DP>(a.out3, r, L - row0, hdo, 1.f, stage, w.lane);
+            park_rows<T, DP>(Kr, row0, hq, sc, w.l16, w.g);
+            park_rows<T, DP>(gKr, row0, hdo, 1.f, w.l16, w.g);
         }
+        count_up(cnt, w.lane);
 
         // ---- col pass: own = keys; hK, hV from the tiles
         f32x4 hk[LY::NT], hv[LY::NT];
@@ -1496,22 +1576,16 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
         }
         lds_barrier();  // B
         if (active) {
-            const int64_t r = ((int64_t)s * L + row0) * DP;
-            if (more) {
-#pragma unroll
-                for (int t = 0; t < LY::NT; ++t) {
-                    pend_k[t] = pack4<T>(hk[t] * sc);
-                    pend_v[t] = pack4<T>(hv[t]);
-                }
-                pend_r = r;
-                pend = true;
-            } else {
-                store_acc_staged<T, DP>(a.out1, r, L - row0, hk, sc, stage, w.lane);
-                store_acc_staged<T, DP>(a.out2, r, L - row0, hv, 1.f, stage, w.lane);
-            }
+            park_rows<T, DP>(park, row0, hk, sc, w.l16, w.g);
+            park_rows<T, DP>(park + R::RB, row0, hv, 1.f, w.l16, w.g);
         }
+        count_up(cnt + 1, w.lane);
         if (!more) break;
-        lds_barrier();  // C
+        // this wave's Q, gQ, dO rows of the next slice into their regions: the next col pass reads them after
+        // barrier A, the next row pass takes them from the registers
+        nx.clear(live);
+        nx.put(Qr, gQr, Or, row0, lo);
         s = n;
+        ++it;
     }
 }
