@@ -1202,10 +1202,10 @@ template <typename T, int DP, int NCH, bool HALF> __global__ __launch_bounds__(5
 //   compute waves                                   loader waves
 //   row pass (s); fetch own rows (n)                load K, gK, V, gV of n into registers; store hK, hV of s - G
 //   --- barrier A: tiles complete, K, gK, V, gV (s) no longer read
-//   hQ, hdO rows (s) -> K, gK regions; count        wait for the count; read them; write K, gK, V, gV (n);
-//   col pass (s)                                    store hQ, hdO (s)
+//   hQ, hdO rows (s) -> K, gK regions; count        wait for the count; read them; write K, gK, V, gV (n)
+//   col pass (s)
 //   --- barrier B: tiles and Q, gQ, dO (s) no longer read; K, gK, V, gV (n) in place
-//   hK, hV rows (s) -> tile area; count             wait for the count; read them; count
+//   hK, hV rows (s) -> tile area; count             store hQ, hdO (s); wait for the count; read them; count
 //   own rows of Q, gQ, dO (n) -> regions; row pass (n), its first tile write after the loaders' count
 // Every counter wait is bounded (SPIN_MAX polls), so no wave can wait forever.
 // =====================================================================================================================
@@ -1435,8 +1435,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
             wait_count(cnt, R::NWC * (it + 1));
             ld.take(Kr);  // hQ, hdO of s from the K, gK regions
             if (more) ld.put_k4(smem, L);
-            ld.store(a.out0, a.out3, s, L);
             lds_barrier();  // B
+            ld.store(a.out0, a.out3, s, L);  // after B: the segment before it gates the next row pass
             wait_count(cnt + 1, R::NWC * (it + 1));
             ld.take(park);  // hK, hV of s
             count_up(cnt + 2, w.lane);
