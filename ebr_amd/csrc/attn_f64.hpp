@@ -17,7 +17,7 @@
 constexpr int F64_ROWS = 16;
 constexpr int F64_TILE = 16;
 constexpr int F64_THREADS = 256;
-constexpr int F64_DMAX = 128;
+constexpr int F64_DMAX = DMAX_F64;
 constexpr int F64_NACC = F64_DMAX / 16;  // D-wide accumulators per thread
 
 // Rows [r0, r0 + 16) of a strided slice into LDS (pitch D); rows past L are 0.

@@ -37,6 +37,8 @@ typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 constexpr int CH = 32;                      // other-side rows per LDS chunk
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int STAT_MAX = 128;               // longest L handled by the one-workgroup-per-(b,h) kernels
+constexpr int DMAX_WIDE = 256;              // widest head dim, 16-bit and fp32 (above 128: the streamed kernels)
+constexpr int DMAX_F64 = 128;               // widest head dim of the fp64 kernels
 
 template <typename T> struct ET;
 
@@ -91,7 +93,11 @@ template <typename T, int DP> struct Lay {
     static constexpr int PN = DP + ET<T>::PADN;          // natural row pitch (elements)
     static constexpr int PT = CH + ET<T>::PADT;          // transposed row pitch (elements)
     static constexpr int NATB = CH * PN * (int)sizeof(T);  // bytes of one natural chunk
-    static constexpr int TRB = DP * PT * (int)sizeof(T);   // bytes of one transposed chunk
+    // fp32 above DP = 128: a transposed copy of each chunk does not fit beside the natural one (the backward of the
+    // backward stages four tensors), so seq-contractions read their A operand from the natural rows, one element per
+    // k slot, and a tensor wanted in both layouts is staged once.
+    static constexpr bool NATSEQ = ET<T>::F32 && DP > 128;
+    static constexpr int TRB = NATSEQ ? 0 : DP * PT * (int)sizeof(T);  // bytes of one transposed chunk
     static_assert(DP % CW == 0, "DP must be a multiple of the d-chunk width");
     static_assert(NATB % 16 == 0 && TRB % 16 == 0, "LDS regions must stay 16-byte aligned");
 };
@@ -284,11 +290,20 @@ template <> struct SeqA<float> {
     f32x4 h0, h1;
 };
 
-// A operand of d tile t: lane (d = 16 t + l16, group g).
+// A operand of d tile t: lane (d = 16 t + l16, group g). Under NATSEQ, Xt holds the chunk's natural rows.
 template <typename T, int DP> __device__ __forceinline__ SeqA<T> read_seqa(const T* Xt, int t, int l16, int g) {
     using LY = Lay<T, DP>;
-    const T* p = Xt + (16 * t + l16) * LY::PT;
     SeqA<T> a;
+    if constexpr (LY::NATSEQ) {
+        const T* q = Xt + 16 * t + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            a.h0[r] = q[(4 * g + r) * LY::PN];
+            a.h1[r] = q[(16 + 4 * g + r) * LY::PN];
+        }
+        return a;
+    }
+    const T* p = Xt + (16 * t + l16) * LY::PT;
     if constexpr (ET<T>::F32) {
         a.h0 = *reinterpret_cast<const f32x4*>(p + 4 * g);
         a.h1 = *reinterpret_cast<const f32x4*>(p + 16 + 4 * g);
@@ -350,7 +365,8 @@ template <typename T, int DP, int N> struct Stage {
         }
     }
 
-    // Xn[t] / Xt[t] may be null (that layout is not wanted for tensor t).
+    // Xn[t] / Xt[t] may be null (that layout is not wanted for tensor t). Under NATSEQ, Xt[t] takes natural rows too
+    // and may alias Xn[t].
     __device__ __forceinline__ void store(T* const (&Xn)[N], T* const (&Xt)[N], int tid, int nthr) const {
 #pragma unroll
         for (int i = 0; i < ITEMS; ++i) {
@@ -363,7 +379,9 @@ template <typename T, int DP, int N> struct Stage {
 #pragma unroll
             for (int t = 0; t < N; ++t) {
                 if (Xn[t]) *reinterpret_cast<u32x4*>(Xn[t] + x * LY::PN + d0) = r[t][i];
-                if (Xt[t]) {
+                if constexpr (LY::NATSEQ) {
+                    if (Xt[t] && Xt[t] != Xn[t]) *reinterpret_cast<u32x4*>(Xt[t] + x * LY::PN + d0) = r[t][i];
+                } else if (Xt[t]) {
                     T* p = Xt[t] + d0 * LY::PT + col;
                     if constexpr (ET<T>::F32) {
                         const f32x4 e = __builtin_bit_cast(f32x4, r[t][i]);

@@ -103,9 +103,10 @@ __device__ __forceinline__ void store_rows(void* out, int64_t row_off, const f32
 // Forward (row pass): online softmax over 32-key chunks.
 // =====================================================================================================================
 
-template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd(Args a) {
+// Wider rows than DP = 128 run 256-thread workgroups (one wave per SIMD, every register for the wave).
+template <typename T, int DP> __global__ __launch_bounds__(DP > 128 ? 256 : 512) void k_fwd(Args a) {
     using LY = Lay<T, DP>;
-    __shared__ __align__(16) unsigned char smem[LY::NATB + LY::TRB];
+    __shared__ __align__(16) unsigned char smem[LY::NATB + (LY::NATSEQ ? LY::NATB : LY::TRB)];
     T* Kn = reinterpret_cast<T*>(smem);
     T* Vt = reinterpret_cast<T*>(smem + LY::NATB);
     const WaveIds w = wave_ids();
@@ -183,7 +184,9 @@ template <typename T, int DP> __global__ __launch_bounds__(512) void k_fwd(Args 
 template <typename T, int DP> __device__ __forceinline__ T* nat_tile(unsigned char* smem, int i) {
     return reinterpret_cast<T*>(smem + i * Lay<T, DP>::NATB);
 }
+// Transposed tile i; under NATSEQ the natural tile of the same tensor (tensor i of a stage has natural tile i).
 template <typename T, int DP> __device__ __forceinline__ T* tr_tile(unsigned char* smem, int nn, int i) {
+    if constexpr (Lay<T, DP>::NATSEQ) return nat_tile<T, DP>(smem, i);
     return reinterpret_cast<T*>(smem + nn * Lay<T, DP>::NATB + i * Lay<T, DP>::TRB);
 }
 
@@ -780,7 +783,7 @@ static bool struct_strides_fit(const Args& a) {
 static int check_shape(int dtype, int B, int H, int L, int D) {
     if (dtype != EBR_DTYPE_F32 && dtype != EBR_DTYPE_BF16 && dtype != EBR_DTYPE_F16 && dtype != EBR_DTYPE_F64)
         return EBR_ERR_DTYPE;
-    if (B < 1 || H < 1 || L < 1 || D < 1 || D > 128) return EBR_ERR_SHAPE;
+    if (B < 1 || H < 1 || L < 1 || D < 1 || D > (dtype == EBR_DTYPE_F64 ? DMAX_F64 : DMAX_WIDE)) return EBR_ERR_SHAPE;
     const int vec = dtype == EBR_DTYPE_F64 ? 1 : (dtype == EBR_DTYPE_F32 ? 4 : 8);
     if (D % vec) return EBR_ERR_SHAPE;
     if ((int64_t)B * H * L >= ((int64_t)1 << 31)) return EBR_ERR_SHAPE;
@@ -849,16 +852,19 @@ static int dispatch(int dtype, int D, Rest&&... rest) {
         if (D <= 16) return F<float, 16>::run(rest...);
         if (D <= 32) return F<float, 32>::run(rest...);
         if (D <= 64) return F<float, 64>::run(rest...);
-        return F<float, 128>::run(rest...);
+        if (D <= 128) return F<float, 128>::run(rest...);
+        return F<float, DMAX_WIDE>::run(rest...);
     }
     if (dtype == EBR_DTYPE_BF16) {
         if (D <= 32) return F<__bf16, 32>::run(rest...);
         if (D <= 64) return F<__bf16, 64>::run(rest...);
-        return F<__bf16, 128>::run(rest...);
+        if (D <= 128) return F<__bf16, 128>::run(rest...);
+        return F<__bf16, DMAX_WIDE>::run(rest...);
     }
     if (D <= 32) return F<_Float16, 32>::run(rest...);
     if (D <= 64) return F<_Float16, 64>::run(rest...);
-    return F<_Float16, 128>::run(rest...);
+    if (D <= 128) return F<_Float16, 128>::run(rest...);
+    return F<_Float16, DMAX_WIDE>::run(rest...);
 }
 
 // The long-sequence kernels (16-bit inputs, L > 128): D a full chunk width, 32-bit buffer offsets per slice.
@@ -911,7 +917,7 @@ static bool plan_allows(const Args& a, int f) { return a.plan == EBR_PLAN_AUTO |
 template <typename T, int DP> struct FwdLaunch {
     static int run(Args a, hipStream_t s) {
         const int64_t bh = (int64_t)a.B * a.H;
-        if constexpr (!ET<T>::F32) {
+        if constexpr (!ET<T>::F32 && DP <= 128) {
             if (plan_allows(a, EBR_PLAN_RESIDENT) && resident_shape(a, DP, 2, false)) {
                 a.nblk = 1;
                 const dim3 grid((int)bh), block(fused_threads(a.L));
@@ -924,7 +930,7 @@ template <typename T, int DP> struct FwdLaunch {
                 return launch_rc();
             }
         }
-        if constexpr (!ET<T>::F32) {
+        if constexpr (!ET<T>::F32 && DP <= 128) {
             if (plan_allows(a, EBR_PLAN_LONG) && long_shape(a, DP, false)) {  // streamed stages, a loader wave
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
@@ -939,7 +945,7 @@ template <typename T, int DP> struct FwdLaunch {
         }
         if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
         int grid, threads;
-        if (fused_shape(a.L)) {
+        if (DP <= 128 && fused_shape(a.L)) {
             a.nblk = 1;
             a.xcd_remap = 0;
             grid = (int)bh;
@@ -955,7 +961,7 @@ template <typename T, int DP> struct FwdLaunch {
 template <typename T, int DP> struct BwdLaunch {
     static int run(Args a, hipStream_t s) {
         const int64_t bh = (int64_t)a.B * a.H;
-        if constexpr (!ET<T>::F32) {
+        if constexpr (!ET<T>::F32 && DP <= 128) {
             a.gq = a.gk = a.gv = a.dO;  // only q, k, v, dO are read
             if ((plan_allows(a, EBR_PLAN_PERSISTENT) || a.plan == EBR_PLAN_RESIDENT) &&
                 resident_shape(a, DP, 2, true)) {
@@ -1034,11 +1040,13 @@ template <typename T, int DP> struct BwdLaunch {
             }
         }
         if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
-        if (fused_shape(a.L)) {
-            a.nblk = 1;
-            a.xcd_remap = 0;
-            hipLaunchKernelGGL((k_bwd_fused<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
-            return launch_rc();
+        if constexpr (DP <= 128) {  // wider rows take the two launches at any L (512-thread workgroups would spill)
+            if (fused_shape(a.L)) {
+                a.nblk = 1;
+                a.xcd_remap = 0;
+                hipLaunchKernelGGL((k_bwd_fused<T, DP>), dim3((int)bh), dim3(fused_threads(a.L)), 0, s, a);
+                return launch_rc();
+            }
         }
         int grid, threads;
         plan_stream(a, bh, grid, threads);
@@ -1053,7 +1061,16 @@ template <typename T, int DP> struct BwdLaunch {
 template <typename T, int DP> struct BbLaunch {
     static int run(Args a, hipStream_t s) {
         const int64_t bh = (int64_t)a.B * a.H;
-        if (fused_shape(a.L)) {
+        if constexpr (DP > 128) {  // wider rows: the two streamed launches at any L
+            if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
+            int grid, threads;
+            plan_stream(a, bh, grid, threads);
+            hipLaunchKernelGGL((k_bb_row<T, DP>), dim3(grid), dim3(threads), 0, s, a);
+            const int rc = launch_rc();
+            if (rc) return rc;
+            hipLaunchKernelGGL((k_bb_col<T, DP>), dim3(grid), dim3(threads), 0, s, a);
+            return launch_rc();
+        } else if (fused_shape(a.L)) {
             a.nblk = 1;
             a.xcd_remap = 0;
             const dim3 grid((int)bh), block(fused_threads(a.L));
@@ -1159,8 +1176,8 @@ const char* ebr_attn_error_string(int code) {
         case EBR_OK: return "ok";
         case EBR_ERR_DTYPE: return "unsupported dtype (expected fp32, bf16, fp16 or fp64)";
         case EBR_ERR_SHAPE:
-            return "unsupported shape (need B, H, L >= 1, B*H*L < 2^31, D <= 128 and a multiple of 8 for 16-bit "
-                   "or 4 for fp32)";
+            return "unsupported shape (need B, H, L >= 1, B*H*L < 2^31, D <= 256 and a multiple of 8 for 16-bit "
+                   "or 4 for fp32, D <= 128 for fp64)";
         case EBR_ERR_ALIGN:
             return "row start not 16-byte aligned (8-byte for fp64) (base pointer or a B/H/L stride)";
         case EBR_ERR_NULL: return "required pointer is NULL";
@@ -1176,9 +1193,8 @@ const char* ebr_attn_error_string(int code) {
 }
 
 int64_t ebr_attn_scratch_bytes(int op, int B, int H, int L, int D) {  // fp64 calls need none
-    (void)D;
     if (B < 1 || H < 1 || L < 1) return 0;
-    if (fused_shape(L)) return 0;
+    if (fused_shape(L) && D <= 128) return 0;  // one workgroup per (b, h): no statistics leave it
     const int64_t bhl = (int64_t)B * H * L;
     if (op == EBR_OP_BWD) return bhl * 4;
     if (op == EBR_OP_BWD_BWD) return 3 * bhl * 4;

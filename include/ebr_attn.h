@@ -18,7 +18,8 @@
  *   - The caller owns every buffer; the library allocates nothing and keeps no pointer after returning.
  *   - Return value: 0 on success, otherwise an EBR_ERR_* code or EBR_ERR_HIP_BASE + hipError_t;
  *     ebr_attn_error_string() describes it. Argument checks run before anything is enqueued.
- *   - Supported shapes: B, H, L >= 1; D <= 128 and a multiple of 8 (16-bit) or 4 (fp32); any D for fp64.
+ *   - Supported shapes: B, H, L >= 1; D <= 256 and a multiple of 8 (16-bit) or 4 (fp32); any D <= 128 for fp64.
+ *     D above 128 runs the two streamed launches (EBR_PLAN_GENERIC) at every L.
  *   - fp64 runs exact fp64 vector-ALU kernels (the reference's fp64 path serves gradcheck shapes) and needs no
  *     scratch.
  */
@@ -102,9 +103,9 @@ int ebr_attn_bwd_bwd(int dtype, int B, int H, int L, int D, float scale,
  * EBR_ERR_PLAN before anything is enqueued; fp64 takes EBR_PLAN_AUTO only. */
 enum {
     EBR_PLAN_AUTO = 0,
-    EBR_PLAN_GENERIC = 1,    /* any of fp32, bf16, fp16: one (b, h) per workgroup up to L = 128, two launches above */
+    EBR_PLAN_GENERIC = 1,    /* fp32, bf16, fp16: one (b, h) per workgroup up to L = 128 (D <= 128), else two launches */
     EBR_PLAN_RESIDENT = 2,   /* bf16 / fp16, L <= 128, D of 32, 64 or 128: one (b, h) per workgroup, operands in LDS */
-    EBR_PLAN_PERSISTENT = 3, /* bf16 / fp16, L <= 128 (bwd, bwd_bwd): persistent workgroups with loader waves */
+    EBR_PLAN_PERSISTENT = 3, /* bf16 / fp16, L <= 128, D <= 128 (bwd, bwd_bwd): persistent workgroups, loader waves */
     EBR_PLAN_LONG = 4,       /* bf16 / fp16, L > 128: 64-row stages streamed by a loader wave (D 32, 64; fwd 128) */
 };
 

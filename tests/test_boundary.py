@@ -212,6 +212,11 @@ def test_plan_override_keys_and_values(monkeypatch):
     monkeypatch.setattr(kernels, "PLAN_OVERRIDE", dict(ref81, fwd=(64, 64, 4, 3), bwd_mode="two", bob_mode="two"))
     assert [kernels._plan(k, 900) for k in ("fwd", "bwd_mode", "bob_mode")] == [_capi.PLAN_AUTO] * 3
     assert [kernels._plan(k, 81) for k in ("bwd_mode", "bob_mode")] == [_capi.PLAN_GENERIC] * 2
+    # above D = 128 every shape takes the two streamed launches: "two" is the library's choice, "single" has no plan
+    assert [kernels._plan(k, 81, 256) for k in ("bwd_mode", "bob_mode")] == [_capi.PLAN_AUTO] * 2
+    monkeypatch.setattr(kernels, "PLAN_OVERRIDE", ref81)
+    with pytest.raises(ValueError, match="one-launch"):
+        kernels._plan("bwd_mode", 81, 192)
     with pytest.raises(ValueError, match="GPU tensors"):  # a valid dictionary reaches the usual checks
         kernels.attn_fwd(q, q, q, 0.5)
 
@@ -284,8 +289,11 @@ def test_kernel_head_dims_pad_to_the_row_vector():
     assert ops.kernel_head_dim(torch.float16, 1) == 8 and ops.kernel_head_dim(torch.float32, 36) == 36
     assert ops.kernel_head_dim(torch.float32, 37) == 40 and ops.kernel_head_dim(F64, 37) == 37
     assert ops.kernel_head_dim(torch.bfloat16, 121) == 128
+    assert ops.kernel_head_dim(torch.bfloat16, 129) == 136 and ops.kernel_head_dim(torch.float32, 255) == 256
     with pytest.raises(ValueError):
-        ops.kernel_head_dim(torch.bfloat16, 129)
+        ops.kernel_head_dim(torch.bfloat16, 257)
+    with pytest.raises(ValueError):
+        ops.kernel_head_dim(F64, 129)
 
 
 def test_zero_head_columns_change_nothing():

@@ -79,7 +79,8 @@ def _fwd(dtype=1, B=1, H=1, L=4, D=64, q=P, qs=(0, 0, 64), o=P, lse=P):
         (dict(dtype=-1), 1),
         (dict(dtype=3, D=129), 2),  # fp64: any D up to 128
         (dict(dtype=3, q=P + 4), 3),  # fp64 rows need 8-byte alignment
-        (dict(D=136), 2),  # D > 128
+        (dict(D=264), 2),  # D > 256
+        (dict(dtype=0, D=260), 2),  # fp32: D > 256
         (dict(D=60), 2),  # not a multiple of 8 for bf16
         (dict(dtype=0, D=62), 2),  # not a multiple of 4 for fp32
         (dict(L=0), 2),

@@ -128,6 +128,40 @@ def test_fp16(cuda, L):
     _case(2, 2, L, 64, torch.float16, cuda, seed=5)
 
 
+# Head dims above 128 (the reference pads any D to a power of two, triton_kernels.py:587-589): the streamed two-launch
+# kernels at 256-wide rows, for every L; fp32 reads its seq-contraction operands from the natural rows there. 136 and
+# 130 / 132 are padded to 256-wide rows with zero columns; L = 1 checks the known answer, 17 a ragged single chunk,
+# 100 several row blocks, 150 a ragged last chunk.
+@pytest.mark.parametrize("L", [1, 17, 100, 150])
+@pytest.mark.parametrize("D,dtype", [(256, torch.bfloat16), (192, torch.float16), (136, torch.bfloat16),
+                                     (256, torch.float32), (132, torch.float32)])
+def test_wide_head_dims(cuda, L, D, dtype):
+    _case(2, 2, L, D, dtype, cuda, seed=D + L)
+
+
+@pytest.mark.parametrize("D,dtype", [(130, torch.bfloat16), (256, torch.bfloat16), (252, torch.float32)])
+def test_wide_head_dims_strided(cuda, D, dtype):
+    """Views of a fused [B, L, 3, H, D] projection on the GPU (row stride 3 H D, not contiguous); 130 and 252 are
+    also padded by the ops."""
+    _say(f"wide D={D} {str(dtype).split('.')[-1]} strided views")
+    B, H, L = 2, 2, 70
+    g = torch.Generator("cpu").manual_seed(D)
+    qkv = (torch.randn(B, L, 3, H, D, generator=g) * 0.125).to(dtype)
+    do, gq, gk, gv = (torch.randn(B, H, L, D, generator=g).to(dtype) for _ in range(4))
+    qkv_d = qkv.to(cuda)
+    q, k, v = (qkv_d[:, :, i].transpose(1, 2) for i in range(3))
+    assert not q.is_contiguous()
+    dod, gqd, gkd, gvd = (t.to(cuda) for t in (do, gq, gk, gv))
+    scale = D**-0.5
+    o, lse = torch.ops.ebr_fused.attn_fwd(q, k, v, scale)
+    dq, dk, dv = torch.ops.ebr_fused.attn_bwd(q, k, v, o, lse, dod, scale)
+    hs = torch.ops.ebr_fused.attn_bwd_bwd(q, k, v, o, lse, dod, dq, gqd, gkd, gvd, scale)
+    got = [x.cpu() for x in (o, lse, dq, dk, dv, *hs)]
+    qc, kc, vc = (qkv[:, :, i].transpose(1, 2).contiguous() for i in range(3))
+    ref = _oracle_all(qc, kc, vc, do, gq, gk, gv, scale, o=got[0], lse=got[1])
+    _compare(got, ref, dtype, f"wide D={D} strided")
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # BASELINE configurations
 # ---------------------------------------------------------------------------------------------------------------------
@@ -426,8 +460,11 @@ def test_bad_arguments_raise(cuda):
         torch.ops.ebr_fused.attn_fwd(q, q.half(), q, 0.125)
     with pytest.raises(TypeError):
         torch.ops.ebr_fused.attn_fwd(q.to(torch.int32), q.to(torch.int32), q.to(torch.int32), 0.125)
-    with pytest.raises(ValueError):  # D > 128: the kernels' registers and LDS hold at most 128 per row
-        x = torch.randn(1, 1, 4, 136, device=cuda)
+    with pytest.raises(ValueError):  # D > 256: no kernels that wide
+        x = torch.randn(1, 1, 4, 264, device=cuda)
+        torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
+    with pytest.raises(ValueError):  # fp64 kernels: D <= 128
+        x = torch.randn(1, 1, 4, 136, device=cuda, dtype=torch.float64)
         torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
     with pytest.raises(ValueError):  # rows but no head dim
         x = torch.randn(1, 1, 4, 0, device=cuda)
