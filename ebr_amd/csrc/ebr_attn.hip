@@ -1022,7 +1022,7 @@ template <typename T, int DP> struct BwdLaunch {
                 return launch_rc();
             }
         }
-        if constexpr (!ET<T>::F32 && DP <= 64) {
+        if constexpr (!ET<T>::F32 && DP <= 128) {
             if (plan_allows(a, EBR_PLAN_LONG) && long_shape(a, DP, true)) {  // k_bwd_long_row, k_bwd_long_col
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
@@ -1114,12 +1114,15 @@ template <typename T, int DP> struct BbLaunch {
             }
             return launch_rc();
         }
-        if constexpr (!ET<T>::F32 && DP <= 64) {
+        if constexpr (!ET<T>::F32 && DP <= 128) {
             if (plan_allows(a, EBR_PLAN_LONG) && long_shape(a, DP, true)) {  // k_bb_long_row, k_bb_long_col
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
-                    constexpr int NWR = NW == LONG_WAVES_WIDE ? BB_ROW_WAVES_WIDE : NW;
-                    constexpr int STG = NW == LONG_WAVES_WIDE ? BB_ROW_STAGE_WIDE : BB_ROW_STAGE;
+                    // D = 128: the row kernel keeps the col kernel's waves and 64-row stages (two 128-row stages of
+                    // four 256-byte-row tensors would take 256 KB of LDS)
+                    constexpr bool WIDE = NW == LONG_WAVES_WIDE && DP <= 64;
+                    constexpr int NWR = WIDE ? BB_ROW_WAVES_WIDE : NW;
+                    constexpr int STG = WIDE ? BB_ROW_STAGE_WIDE : BB_ROW_STAGE;
                     {  // the row kernel has a row blocking of its own; the col kernel reads only its statistics
                         Args ar = a;
                         using CR = LongCfg<T, DP, NWR>;

@@ -106,7 +106,7 @@ enum {
     EBR_PLAN_GENERIC = 1,    /* fp32, bf16, fp16: one (b, h) per workgroup up to L = 128 (D <= 128), else two launches */
     EBR_PLAN_RESIDENT = 2,   /* bf16 / fp16, L <= 128, D of 32, 64 or 128: one (b, h) per workgroup, operands in LDS */
     EBR_PLAN_PERSISTENT = 3, /* bf16 / fp16, L <= 128, D <= 128 (bwd, bwd_bwd): persistent workgroups, loader waves */
-    EBR_PLAN_LONG = 4,       /* bf16 / fp16, L > 128: 64-row stages streamed by a loader wave (D 32, 64; fwd 128) */
+    EBR_PLAN_LONG = 4,       /* bf16 / fp16, L > 128, D of 32, 64 or 128: 64-row stages streamed by a loader wave */
 };
 
 /* ebr_attn_fwd, ebr_attn_bwd and ebr_attn_bwd_bwd with the kernel family forced by plan (EBR_PLAN_*); same

@@ -609,8 +609,12 @@ PLAN_CASES = [
     (2, 2, 200, 64, torch.bfloat16, {"fwd": ("generic long", "resident persistent"),
                                      "bwd_mode": ("generic long", "resident persistent"),
                                      "bob_mode": ("generic long", "resident persistent")}),
-    (2, 2, 200, 128, torch.bfloat16, {"fwd": ("generic long", "resident"), "bwd_mode": ("generic", "long"),
-                                      "bob_mode": ("generic", "long")}),
+    (2, 2, 200, 128, torch.bfloat16, {"fwd": ("generic long", "resident"),
+                                      "bwd_mode": ("generic long", "resident persistent"),
+                                      "bob_mode": ("generic long", "resident persistent")}),
+    (2, 2, 81, 256, torch.bfloat16, {"fwd": ("generic", "resident long"),
+                                     "bwd_mode": ("generic", "resident persistent long"),
+                                     "bob_mode": ("generic", "resident persistent long")}),
     (2, 2, 81, 64, torch.float32, {"fwd": ("generic", "resident long"), "bwd_mode": ("generic", "persistent"),
                                    "bob_mode": ("generic", "resident persistent long")}),
 ]
