@@ -1027,6 +1027,7 @@ template <typename T, int DP> struct BwdLaunch {
                 auto run = [&](auto nw) {
                     constexpr int NW = decltype(nw)::value;
                     using C = LongCfg<T, DP, NW>;
+                    if (!a.stats) return (int)EBR_ERR_SCRATCH;  // the row kernel publishes its statistics there
                     plan_long(a, bh, C::ROWS);
                     const dim3 grid((int)(bh * a.nblk)), block(C::THREADS);
                     hipLaunchKernelGGL((k_bwd_long_row<T, DP, NW>), grid, block, 0, s, a);
@@ -1049,6 +1050,7 @@ template <typename T, int DP> struct BwdLaunch {
             }
         }
         int grid, threads;
+        if (!a.stats) return (int)EBR_ERR_SCRATCH;  // the row kernel publishes its statistics there
         plan_stream(a, bh, grid, threads);
         hipLaunchKernelGGL((k_bwd_row<T, DP>), dim3(grid), dim3(threads), 0, s, a);
         int rc = launch_rc();
@@ -1064,6 +1066,7 @@ template <typename T, int DP> struct BbLaunch {
         if constexpr (DP > 128) {  // wider rows: the two streamed launches at any L
             if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
             int grid, threads;
+            if (!a.stats) return (int)EBR_ERR_SCRATCH;  // the row kernel publishes its statistics there
             plan_stream(a, bh, grid, threads);
             hipLaunchKernelGGL((k_bb_row<T, DP>), dim3(grid), dim3(threads), 0, s, a);
             const int rc = launch_rc();
@@ -1126,6 +1129,7 @@ template <typename T, int DP> struct BbLaunch {
                     {  // the row kernel has a row blocking of its own; the col kernel reads only its statistics
                         Args ar = a;
                         using CR = LongCfg<T, DP, NWR>;
+                        if (!a.stats) return (int)EBR_ERR_SCRATCH;  // the row kernel publishes its statistics there
                         plan_long(ar, bh, CR::ROWS);
                         hipLaunchKernelGGL((k_bb_long_row<T, DP, NWR, STG>), dim3((int)(bh * ar.nblk)),
                                            dim3(CR::THREADS), 0, s, ar);
@@ -1144,6 +1148,7 @@ template <typename T, int DP> struct BbLaunch {
         }
         if (!plan_allows(a, EBR_PLAN_GENERIC)) return EBR_ERR_PLAN;
         int grid, threads;
+        if (!a.stats) return (int)EBR_ERR_SCRATCH;  // the row kernel publishes its statistics there
         plan_stream(a, bh, grid, threads);
         hipLaunchKernelGGL((k_bb_row<T, DP>), dim3(grid), dim3(threads), 0, s, a);
         int rc = launch_rc();
