@@ -38,7 +38,7 @@ constexpr int CH = 32;                      // other-side rows per LDS chunk
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int STAT_MAX = 128;               // longest L handled by the one-workgroup-per-(b,h) kernels
 constexpr int DMAX_WIDE = 256;              // widest head dim, 16-bit and fp32 (above 128: the streamed kernels)
-constexpr int DMAX_F64 = 128;               // widest head dim of the fp64 kernels
+constexpr int DMAX_F64 = 256;               // widest head dim of the fp64 kernels
 
 template <typename T> struct ET;
 

@@ -1185,7 +1185,7 @@ const char* ebr_attn_error_string(int code) {
         case EBR_ERR_DTYPE: return "unsupported dtype (expected fp32, bf16, fp16 or fp64)";
         case EBR_ERR_SHAPE:
             return "unsupported shape (need B, H, L >= 1, B*H*L < 2^31, D <= 256 and a multiple of 8 for 16-bit "
-                   "or 4 for fp32, D <= 128 for fp64)";
+                   "or 4 for fp32, any D <= 256 for fp64)";
         case EBR_ERR_ALIGN:
             return "row start not 16-byte aligned (8-byte for fp64) (base pointer or a B/H/L stride)";
         case EBR_ERR_NULL: return "required pointer is NULL";

@@ -17,8 +17,9 @@ Where each call runs (``route``):
 Head dims the kernels do not take natively (16-bit D not a multiple of 8, fp32 D not a multiple of 4) are zero-padded
 to the next such width and the outputs cut back: zero columns add nothing to any score and produce zero columns in
 every output, so the result is exact (the reference pads the same way inside its kernels, ``triton_kernels.py:587-589``).
-Head dims up to 256 run on the GPU (fp64: up to 128); wider ones raise ``ValueError``. Above 128 the 16-bit and fp32
-calls take the streamed two-launch kernels at every N (a 16-row tile of 256-wide rows needs a whole SIMD's registers).
+Head dims up to 256 run on the GPU; wider ones raise ``ValueError``. Above 128 the 16-bit and fp32 calls take the
+streamed two-launch kernels at every N (a 16-row tile of 256-wide rows needs a whole SIMD's registers), and fp64 its
+kernels with 8-row tiles.
 
 Autograd: ``_FusedAttn`` (its backward is ``_FusedAttnBwd``) and ``_FusedAttnBwd`` (its backward is attn_bwd_bwd),
 both with ``setup_context`` as ``torch.func`` requires; ``fused_attention`` stays a single dynamo node through
@@ -39,8 +40,7 @@ from ebr_amd.fused_attn.loader import hip_library, mode
 
 Tensor = torch.Tensor
 
-MAX_HEAD_DIM = 256  # fp32, bf16, fp16
-MAX_HEAD_DIM_F64 = 128
+MAX_HEAD_DIM = 256
 
 _DTYPE_CODE = {
     torch.float32: _capi.DTYPE_F32,
@@ -117,9 +117,8 @@ def _dtype_code(t: Tensor) -> int:
 def kernel_head_dim(dtype: torch.dtype, d: int) -> int:
     """Width the kernels run a head dim of ``d`` at: ``d`` itself when they take it, else the next multiple of the
     16-byte row vector (8 for 16-bit types, 4 for fp32); fp64 takes any width."""
-    top = MAX_HEAD_DIM_F64 if dtype == torch.float64 else MAX_HEAD_DIM
-    if d < 1 or d > top:
-        raise ValueError(f"fused attention on the GPU takes {dtype} head dims 1..{top}, got {d}")
+    if d < 1 or d > MAX_HEAD_DIM:
+        raise ValueError(f"fused attention on the GPU takes head dims 1..{MAX_HEAD_DIM}, got {d}")
     if dtype == torch.float64:
         return d
     vec = 4 if dtype == torch.float32 else 8

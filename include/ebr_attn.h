@@ -18,7 +18,7 @@
  *   - The caller owns every buffer; the library allocates nothing and keeps no pointer after returning.
  *   - Return value: 0 on success, otherwise an EBR_ERR_* code or EBR_ERR_HIP_BASE + hipError_t;
  *     ebr_attn_error_string() describes it. Argument checks run before anything is enqueued.
- *   - Supported shapes: B, H, L >= 1; D <= 256 and a multiple of 8 (16-bit) or 4 (fp32); any D <= 128 for fp64.
+ *   - Supported shapes: B, H, L >= 1; D <= 256 and a multiple of 8 (16-bit) or 4 (fp32); any D <= 256 for fp64.
  *     D above 128 runs the two streamed launches (EBR_PLAN_GENERIC) at every L.
  *   - fp64 runs exact fp64 vector-ALU kernels (the reference's fp64 path serves gradcheck shapes) and needs no
  *     scratch.

@@ -292,8 +292,9 @@ def test_kernel_head_dims_pad_to_the_row_vector():
     assert ops.kernel_head_dim(torch.bfloat16, 129) == 136 and ops.kernel_head_dim(torch.float32, 255) == 256
     with pytest.raises(ValueError):
         ops.kernel_head_dim(torch.bfloat16, 257)
+    assert ops.kernel_head_dim(F64, 129) == 129
     with pytest.raises(ValueError):
-        ops.kernel_head_dim(F64, 129)
+        ops.kernel_head_dim(F64, 257)
 
 
 def test_zero_head_columns_change_nothing():

@@ -77,7 +77,7 @@ def _fwd(dtype=1, B=1, H=1, L=4, D=64, q=P, qs=(0, 0, 64), o=P, lse=P):
     [
         (dict(dtype=4), 1),  # unknown dtype
         (dict(dtype=-1), 1),
-        (dict(dtype=3, D=129), 2),  # fp64: any D up to 128
+        (dict(dtype=3, D=257), 2),  # fp64: any D up to 256
         (dict(dtype=3, q=P + 4), 3),  # fp64 rows need 8-byte alignment
         (dict(D=264), 2),  # D > 256
         (dict(dtype=0, D=260), 2),  # fp32: D > 256

@@ -61,7 +61,7 @@ def _compare(got, ref, label, L):
 @pytest.mark.parametrize(
     "B,H,L,D",
     [(2, 3, 1, 8), (2, 2, 5, 3), (1, 2, 17, 64), (2, 2, 40, 128), (1, 1, 81, 7), (2, 1, 129, 16), (1, 2, 200, 64),
-     (1, 1, 9, 1), (1, 1, 33, 100)],
+     (1, 1, 9, 1), (1, 1, 33, 100), (1, 2, 17, 136), (2, 1, 40, 200), (1, 1, 70, 256)],
 )
 def test_fp64_matches_oracle(cuda, B, H, L, D):
     _say(f"fp64 B={B} H={H} L={L} D={D}")
@@ -111,12 +111,13 @@ def test_fp64_matches_golden(cuda):
     assert n >= 3
 
 
-def test_fp64_gradcheck_and_gradgradcheck(cuda):
+@pytest.mark.parametrize("shape", [(1, 2, 6, 4), (1, 1, 3, 136)])  # 136: the 8-row kernels of D > 128
+def test_fp64_gradcheck_and_gradgradcheck(cuda, shape):
     """torch.autograd.gradcheck / gradgradcheck of fused_attention on the GPU: the forward, its backward (attn_bwd)
     and the double backward (attn_bwd_bwd) against finite differences of the op itself."""
-    _say("fp64 gradcheck")
+    _say(f"fp64 gradcheck {shape}")
     g = torch.Generator().manual_seed(11)
-    q, k, v = (torch.randn(1, 2, 6, 4, generator=g, dtype=F64).to(cuda).requires_grad_(True) for _ in range(3))
+    q, k, v = (torch.randn(*shape, generator=g, dtype=F64).to(cuda).requires_grad_(True) for _ in range(3))
 
     def f(a, b, c):
         return fused_attention(a, b, c, scale=0.5)

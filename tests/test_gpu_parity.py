@@ -463,8 +463,8 @@ def test_bad_arguments_raise(cuda):
     with pytest.raises(ValueError):  # D > 256: no kernels that wide
         x = torch.randn(1, 1, 4, 264, device=cuda)
         torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
-    with pytest.raises(ValueError):  # fp64 kernels: D <= 128
-        x = torch.randn(1, 1, 4, 136, device=cuda, dtype=torch.float64)
+    with pytest.raises(ValueError):  # fp64 kernels: D <= 256 too
+        x = torch.randn(1, 1, 4, 260, device=cuda, dtype=torch.float64)
         torch.ops.ebr_fused.attn_fwd(x, x, x, 0.1)
     with pytest.raises(ValueError):  # rows but no head dim
         x = torch.randn(1, 1, 4, 0, device=cuda)
