@@ -608,7 +608,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NC
                 constexpr int C = decltype(cc)::value;
                 constexpr bool LAST = C == NCH - 1;
                 const int x0 = C * CH;
-                f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+                // the dP accumulators start at -Dr, so dS = P (dP - Dr) takes one multiply per element
+                f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = {-dr, -dr, -dr, -dr}, d1 = d0;
                 mma_d_sw<T, DP>(p0, Kr, x0, qf, lo);
                 mma_d_sw<T, DP>(p1, Kr, x0 + 16, qf, lo);
                 mma_d_sw<T, DP>(d0, Vr, x0, df, lo);
@@ -618,8 +619,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NC
                     const int x = x0 + 4 * w.g + r;
                     p0[r] = row_p<LAST>(p0[r], sc2, lse2, x, L);  // lse = +inf on padded query rows -> P = 0
                     p1[r] = row_p<LAST>(p1[r], sc2, lse2, x + 16, L);
-                    d0[r] = p0[r] * (d0[r] - dr);
-                    d1[r] = p1[r] * (d1[r] - dr);
+                    d0[r] = p0[r] * d0[r];
+                    d1[r] = p1[r] * d1[r];
                 }
                 const SeqB<T> dsb = make_seqb<T>(d0, d1);
                 if constexpr (R::TILES) {
@@ -663,7 +664,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NC
                     const f32x4 l1 = *reinterpret_cast<const f32x4*>(l2 + x0 + 16 + 4 * w.g);
                     const f32x4 r0 = *reinterpret_cast<const f32x4*>(dr2 + x0 + 4 * w.g);
                     const f32x4 r1 = *reinterpret_cast<const f32x4*>(dr2 + x0 + 16 + 4 * w.g);
-                    f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = p0, d1 = p0;
+                    f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, d0 = -r0, d1 = -r1;
                     mma_d_sw<T, DP>(p0, Qr, x0, kf, lo);
                     mma_d_sw<T, DP>(p1, Qr, x0 + 16, kf, lo);
                     mma_d_sw<T, DP>(d0, Or, x0, vf, lo);
@@ -672,8 +673,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(64 * (2 * NC
                     for (int r = 0; r < 4; ++r) {
                         p0[r] = fast_exp2(fmaf(p0[r], sc2, -l0[r]));  // lse = +inf on padded query rows -> P = 0
                         p1[r] = fast_exp2(fmaf(p1[r], sc2, -l1[r]));
-                        d0[r] = p0[r] * (d0[r] - r0[r]);
-                        d1[r] = p1[r] * (d1[r] - r1[r]);
+                        d0[r] = p0[r] * d0[r];
+                        d1[r] = p1[r] * d1[r];
                     }
                     pb = make_seqb<T>(p0, p1);
                     dsb = make_seqb<T>(d0, d1);
@@ -1485,7 +1486,8 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                 f32x4 p[2], dp[2], at[2], bm[2];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
-                    p[hh] = dp[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    p[hh] = at[hh] = bm[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    dp[hh] = f32x4{-dr, -dr, -dr, -dr};  // dP - Dr, one multiply from dS
                     const int r0 = x0 + 16 * hh;
                     mma_d_sw<T, DP>(p[hh], Kr, r0, qf, lo);
                     mma_d_sw<T, DP>(at[hh], Kr, r0, gqf, lo);
@@ -1499,7 +1501,7 @@ template <typename T, int DP, int NCH> __global__ __launch_bounds__(512) void k_
                     for (int r = 0; r < 4; ++r) {
                         const int e = 4 * hh + r;
                         const float pv = row_p<LAST>(p[hh][r], sc2, lse2, x0 + 16 * hh + 4 * w.g + r, L);
-                        const float dsv = pv * (dp[hh][r] - dr);
+                        const float dsv = pv * dp[hh][r];
                         const float av = at[hh][r] * sc;
                         pf[C][e] = pv;
                         dsf[C][e] = dsv;
