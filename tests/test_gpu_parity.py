@@ -685,13 +685,13 @@ def test_reference_plan_override_values(cuda, case, monkeypatch):
     _compare(got, ref, dtype, f"reference-style plan override case {case}")
 
 
-def _random_cases(n, seed=2024):
+def _random_cases(n, seed=2024, dmin=1, dmax=128):
     g = torch.Generator().manual_seed(seed)
     out = []
     for i in range(n):
         dtype = [torch.float32, torch.bfloat16, torch.float16][int(torch.randint(0, 3, (1,), generator=g))]
         L = int(torch.randint(1, 320, (1,), generator=g))
-        D = int(torch.randint(1, 129, (1,), generator=g))
+        D = int(torch.randint(dmin, dmax + 1, (1,), generator=g))
         B = int(torch.randint(1, 4, (1,), generator=g))
         H = int(torch.randint(1, 4, (1,), generator=g))
         out.append((i, B, H, L, D, dtype))
@@ -703,3 +703,9 @@ def test_random_shapes(cuda, i, B, H, L, D, dtype):
     """Seeded random shapes (any L up to 319, any head dim up to 128, three dtypes, small B and H): whatever plan
     and padding the ops pick, every output matches the oracle."""
     _case(B, H, L, D, dtype, cuda, seed=100 + i)
+
+
+@pytest.mark.parametrize("i,B,H,L,D,dtype", _random_cases(8, seed=77, dmin=129, dmax=256))
+def test_random_wide_shapes(cuda, i, B, H, L, D, dtype):
+    """Seeded random shapes with head dims 129..256 (the 256-wide streamed kernels, padded widths included)."""
+    _case(B, H, L, D, dtype, cuda, seed=300 + i)
