@@ -1,6 +1,7 @@
 // ebr_attn_bwd_bwd_noalloc: the backward of the backward for callers that cannot allocate device memory (code under
 // HIP graph capture, serving loops, harnesses that forbid hipMalloc). It runs exactly the kernels of
-// ebr_attn_bwd_bwd; the fp32 row-statistics scratch those kernels exchange for L > 128 ([3, B, H, L]: Dr, E, T)
+// ebr_attn_bwd_bwd; the fp32 row-statistics scratch those kernels exchange for L > 128 or D > 128 ([3, B, H, L]:
+// Dr, E, T)
 // lives in a fixed device array of this library instead of a caller buffer.
 //
 // The array is a file-scope __device__ variable: every GPU the library runs on holds its own copy, at its own address,

@@ -140,7 +140,7 @@ int ebr_attn_bwd_bwd_plan(int dtype, int B, int H, int L, int D, float scale,
 /* ebr_attn_bwd_bwd without the scratch argument, for callers that cannot allocate device memory: code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc. It has no counterpart in the reference (whose
  * launchers allocate their statistics buffers, models/fused_attn/triton_kernels.py:910-912). Same arguments, kernels
- * and results as ebr_attn_bwd_bwd; the fp32 row statistics that shapes with L > 128 exchange between their two
+ * and results as ebr_attn_bwd_bwd; the fp32 row statistics that shapes with L > 128 (or D > 128) exchange between their two
  * launches ([3, B, H, L], ebr_attn_scratch_bytes) live in a device array of the library, EBR_NOALLOC_SCRATCH_BYTES
  * per GPU, held until the process ends. Shapes that need more return EBR_ERR_NOALLOC_SIZE before anything is
  * enqueued. It calls no allocating routine. Every call on one GPU shares that GPU's array: calls that overlap on one
