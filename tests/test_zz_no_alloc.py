@@ -48,7 +48,8 @@ def _run(lib, entry, B, H, L, D, dtype, seed, dev):
 
 
 @pytest.mark.parametrize("shape", [(6, 8, 900, 64, torch.bfloat16), (2, 4, 300, 64, torch.bfloat16),
-                                   (3, 4, 81, 64, torch.bfloat16), (2, 2, 200, 32, torch.float16)])
+                                   (3, 4, 81, 64, torch.bfloat16), (2, 2, 200, 32, torch.float16),
+                                   (2, 2, 40, 256, torch.bfloat16), (2, 2, 150, 128, torch.bfloat16)])
 def test_noalloc_equals_scratch_entry(cuda, shape):
     B, H, L, D, dtype = shape
     print(f"[case] noalloc B={B} H={H} L={L} D={D} {dtype}", flush=True)
