@@ -398,12 +398,14 @@ def test_verify_second_order_fused(cuda):
     verify_second_order(get_backend("fused"), device=cuda)
 
 
-def test_outputs_do_not_depend_on_stale_memory(cuda):
+@pytest.mark.parametrize("B,H,L,D,dtype", [(4, 4, 150, 64, torch.bfloat16), (8, 4, 81, 64, torch.bfloat16),
+                                           (2, 2, 100, 256, torch.bfloat16), (2, 2, 60, 256, torch.float32),
+                                           (2, 2, 100, 128, torch.float16)])
+def test_outputs_do_not_depend_on_stale_memory(cuda, B, H, L, D, dtype):
     """Two calls with the same inputs after a caching-allocator churn give bit-identical results (no reads of
-    uninitialised memory, no run-to-run nondeterminism)."""
-    B, H, L, D = 4, 4, 150, 64
-    _say("determinism")
-    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, torch.bfloat16, 21)
+    uninitialised memory, no run-to-run nondeterminism): long, persistent, resident and wide-row kernels."""
+    _say(f"determinism B={B} H={H} L={L} D={D} {dtype}")
+    q, k, v, do, gq, gk, gv = _inputs(B, H, L, D, dtype, 21)
     scale = D**-0.5
     a = _hip_all(q, k, v, do, gq, gk, gv, scale, cuda)
     junk = torch.full((64 << 20,), float("nan"), device=cuda)
