@@ -56,6 +56,9 @@ def test_scratch_sizes():
     assert lib.ebr_attn_scratch_bytes(_capi.OP_BWD_BWD, 768, 8, 128, 64) == 0
     assert lib.ebr_attn_scratch_bytes(_capi.OP_BWD, 64, 8, 900, 64) == 64 * 8 * 900 * 4
     assert lib.ebr_attn_scratch_bytes(_capi.OP_BWD_BWD, 64, 8, 900, 64) == 3 * 64 * 8 * 900 * 4
+    # head dims above 128 run the two streamed launches at every L, so short sequences need the statistics too
+    assert lib.ebr_attn_scratch_bytes(_capi.OP_BWD, 2, 4, 40, 256) == 2 * 4 * 40 * 4
+    assert lib.ebr_attn_scratch_bytes(_capi.OP_BWD_BWD, 2, 4, 40, 136) == 3 * 2 * 4 * 40 * 4
 
 
 def _str(*s):
